@@ -1,0 +1,328 @@
+// mxfa_api.cpp -- host side of the C ABI declared in include/mxfa.h.
+//
+// Validates ggml-style descriptors (the same contract ggml_flash_attn_ext
+// asserts), picks a kernel and launches it on the caller's stream:
+//   * split-KV kernel (fa_split.hip) when few query rows share a KV head:
+//     decode (Sq = 1) and short prompts, and Q8_0 K/V;
+//   * MFMA prefill kernel (fa_mfma.hip) for long query runs (prefill, DiT),
+//     preceded by the mask tile classifier when a mask is given.
+// The only memory the engine owns is a per-device, grow-only workspace
+// (split partials, mask tile classes), freed by mxfa_release().
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "mxfa.h"
+#include "mxfa_internal.h"
+
+namespace {
+
+using namespace mxfa;
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+struct Workspace {
+    void *ptr = nullptr;
+    size_t size = 0;
+};
+std::mutex g_ws_mu;
+std::vector<Workspace> g_ws;  // indexed by HIP device id
+
+// Query-run length from which the MFMA prefill kernel is used.
+constexpr int64_t kPrefillMinSq = 64;
+// Workgroups the split kernel aims for before it splits the KV range.
+constexpr int64_t kSplitTargetWgs = 1024;
+constexpr int kSplitKeyQuantum = 128;  // 4 waves x 32 keys
+
+bool is_aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+size_t elem_row_bytes(int type, int64_t ne0) {
+    switch (type) {
+        case MXFA_TYPE_F32: return 4 * (size_t)ne0;
+        case MXFA_TYPE_F16:
+        case MXFA_TYPE_BF16: return 2 * (size_t)ne0;
+        case MXFA_TYPE_Q8_0: return (size_t)(ne0 / 32) * 34;
+        default: return 0;
+    }
+}
+
+size_t type_block_bytes(int type) {
+    switch (type) {
+        case MXFA_TYPE_F32: return 4;
+        case MXFA_TYPE_F16:
+        case MXFA_TYPE_BF16: return 2;
+        case MXFA_TYPE_Q8_0: return 34;
+        default: return 0;
+    }
+}
+
+struct Plan {
+    bool prefill = false;
+    FaArgs args{};
+    int ktype = 0;
+    int n_planes = 0;
+    size_t ws_bytes = 0;
+};
+
+// Full validation.  Returns MXFA_OK, MXFA_ERR_INVALID (malformed) or
+// MXFA_ERR_UNSUPPORTED (well-formed but not handled by these kernels).
+int check(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
+          const mxfa_params *p, const mxfa_tensor *dst) {
+    if (!q || !k || !v || !p) return fail(MXFA_ERR_INVALID, "q, k, v and params are required");
+    for (const mxfa_tensor *t : {q, k, v, mask, dst}) {
+        if (!t) continue;
+        for (int i = 0; i < 4; i++)
+            if (t->ne[i] <= 0) return fail(MXFA_ERR_INVALID, "ne[%d] = %lld must be positive", i, (long long)t->ne[i]);
+    }
+    if (q->type != MXFA_TYPE_F32) return fail(MXFA_ERR_UNSUPPORTED, "q must be F32 (type %d)", q->type);
+    if (k->type != MXFA_TYPE_F16 && k->type != MXFA_TYPE_BF16 && k->type != MXFA_TYPE_Q8_0)
+        return fail(MXFA_ERR_UNSUPPORTED, "k type %d not supported (F16, BF16, Q8_0)", k->type);
+    if (v->type != k->type) return fail(MXFA_ERR_UNSUPPORTED, "k and v types differ (%d, %d)", k->type, v->type);
+    if (q->ne[0] != k->ne[0]) return fail(MXFA_ERR_INVALID, "q->ne[0] != k->ne[0]");
+    if (k->ne[1] != v->ne[1]) return fail(MXFA_ERR_INVALID, "k->ne[1] != v->ne[1]");
+    if (q->ne[0] != kD || v->ne[0] != kD) return fail(MXFA_ERR_UNSUPPORTED, "head size %lld/%lld (only 128)",
+                                                       (long long)q->ne[0], (long long)v->ne[0]);
+    if (k->ne[2] != v->ne[2] || k->ne[3] != v->ne[3])
+        return fail(MXFA_ERR_UNSUPPORTED, "k and v head/batch counts differ");
+    if (q->ne[2] % k->ne[2]) return fail(MXFA_ERR_INVALID, "Nh %% Nkv != 0");
+    if (q->ne[3] % k->ne[3]) return fail(MXFA_ERR_INVALID, "B %% Bk != 0");
+    const int64_t lim = (int64_t)1 << 30;
+    if (q->ne[1] > lim || q->ne[2] > 65535 || q->ne[3] > 65535 || k->ne[1] > lim)
+        return fail(MXFA_ERR_UNSUPPORTED, "dimension too large");
+    if (q->nb[0] != 4) return fail(MXFA_ERR_UNSUPPORTED, "q rows must be contiguous");
+    if (k->nb[0] != type_block_bytes(k->type) || v->nb[0] != type_block_bytes(v->type))
+        return fail(MXFA_ERR_UNSUPPORTED, "k/v rows must be contiguous");
+    if (!q->data || !k->data || !v->data) return fail(MXFA_ERR_INVALID, "NULL data pointer");
+    if (!is_aligned(q->data, 16) || q->nb[1] % 16 || q->nb[2] % 16 || q->nb[3] % 16)
+        return fail(MXFA_ERR_UNSUPPORTED, "q data/strides must be 16-byte aligned");
+    const size_t kv_align = k->type == MXFA_TYPE_Q8_0 ? 4 : 16;
+    for (const mxfa_tensor *t : {k, v})
+        if (!is_aligned(t->data, kv_align) || t->nb[1] % kv_align || t->nb[2] % kv_align || t->nb[3] % kv_align)
+            return fail(MXFA_ERR_UNSUPPORTED, "k/v data/strides must be %zu-byte aligned", kv_align);
+    if (mask) {
+        if (mask->type != MXFA_TYPE_F16) return fail(MXFA_ERR_UNSUPPORTED, "mask must be F16");
+        if (!mask->data) return fail(MXFA_ERR_INVALID, "NULL mask data");
+        if (mask->nb[0] != 2) return fail(MXFA_ERR_UNSUPPORTED, "mask rows must be contiguous");
+        if (mask->ne[0] < k->ne[1]) return fail(MXFA_ERR_INVALID, "mask->ne[0] < Skv");
+        if (mask->ne[1] < q->ne[1]) return fail(MXFA_ERR_INVALID, "mask->ne[1] < Sq");
+        if (q->ne[2] % mask->ne[2] || q->ne[3] % mask->ne[3])
+            return fail(MXFA_ERR_INVALID, "mask does not broadcast over heads/batches");
+        if (!is_aligned(mask->data, 2) || mask->nb[1] % 2 || mask->nb[2] % 2 || mask->nb[3] % 2)
+            return fail(MXFA_ERR_INVALID, "mask misaligned");
+    }
+    if (!(p->scale == p->scale) || !std::isfinite(p->scale)) return fail(MXFA_ERR_INVALID, "scale not finite");
+    if (p->max_bias < 0.0f || !std::isfinite(p->max_bias)) return fail(MXFA_ERR_INVALID, "max_bias invalid");
+    if (!std::isfinite(p->logit_softcap)) return fail(MXFA_ERR_INVALID, "logit_softcap not finite");
+    if (p->prec != MXFA_PREC_DEFAULT && p->prec != MXFA_PREC_F32) return fail(MXFA_ERR_INVALID, "prec %d", p->prec);
+    if (dst) {
+        if (dst->type != MXFA_TYPE_F32) return fail(MXFA_ERR_UNSUPPORTED, "dst must be F32");
+        if (dst->ne[0] != v->ne[0] || dst->ne[1] != q->ne[2] || dst->ne[2] != q->ne[1] || dst->ne[3] != q->ne[3])
+            return fail(MXFA_ERR_INVALID, "dst shape must be [DV, Nh, Sq, B]");
+        const size_t nb1 = 4 * (size_t)dst->ne[0], nb2 = nb1 * dst->ne[1], nb3 = nb2 * dst->ne[2];
+        if (dst->nb[0] != 4 || dst->nb[1] != nb1 || dst->nb[2] != nb2 || dst->nb[3] != nb3)
+            return fail(MXFA_ERR_UNSUPPORTED, "dst must be contiguous");
+        if (!dst->data || !is_aligned(dst->data, 16)) return fail(MXFA_ERR_INVALID, "dst data NULL or misaligned");
+    }
+    return MXFA_OK;
+}
+
+void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
+               const mxfa_params *p, mxfa_tensor *dst, Plan &pl) {
+    FaArgs &a = pl.args;
+    a.q = (const char *)q->data;
+    a.k = (const char *)k->data;
+    a.v = (const char *)v->data;
+    a.mask = mask ? (const char *)mask->data : nullptr;
+    a.dst = dst ? (float *)dst->data : nullptr;
+    a.q_nb1 = (int64_t)q->nb[1]; a.q_nb2 = (int64_t)q->nb[2]; a.q_nb3 = (int64_t)q->nb[3];
+    a.k_nb1 = (int64_t)k->nb[1]; a.k_nb2 = (int64_t)k->nb[2]; a.k_nb3 = (int64_t)k->nb[3];
+    a.v_nb1 = (int64_t)v->nb[1]; a.v_nb2 = (int64_t)v->nb[2]; a.v_nb3 = (int64_t)v->nb[3];
+    if (mask) {
+        a.m_nb1 = (int64_t)mask->nb[1]; a.m_nb2 = (int64_t)mask->nb[2]; a.m_nb3 = (int64_t)mask->nb[3];
+        a.m_ne2 = (int32_t)mask->ne[2]; a.m_ne3 = (int32_t)mask->ne[3];
+    } else {
+        a.m_ne2 = 1; a.m_ne3 = 1;
+    }
+    a.Sq = (int32_t)q->ne[1];
+    a.Nh = (int32_t)q->ne[2];
+    a.B = (int32_t)q->ne[3];
+    a.Skv = (int32_t)k->ne[1];
+    a.Nkv = (int32_t)k->ne[2];
+    a.G = a.Nh / a.Nkv;
+    a.rk3 = (int32_t)(q->ne[3] / k->ne[3]);
+    a.M = a.Sq * a.G;
+    a.scale = p->scale;
+    a.softcap = p->logit_softcap;
+    a.max_bias = p->max_bias;
+    // ALiBi constants as ggml computes them (per-head slopes).
+    const uint32_t n_head = (uint32_t)a.Nh;
+    a.n_head_log2 = 1u << (uint32_t)std::floor(std::log2((double)n_head));
+    a.m0 = std::pow(2.0f, -(p->max_bias) / (float)a.n_head_log2);
+    a.m1 = std::pow(2.0f, -(p->max_bias / 2.0f) / (float)a.n_head_log2);
+    pl.ktype = k->type;
+
+    const bool mask_vec_ok = !mask || (is_aligned(mask->data, 8) && mask->nb[1] % 8 == 0 && mask->nb[2] % 8 == 0 &&
+                                       mask->nb[3] % 8 == 0);
+    pl.prefill = (k->type == MXFA_TYPE_F16 || k->type == MXFA_TYPE_BF16) && a.Sq >= kPrefillMinSq && mask_vec_ok;
+    if (pl.prefill) {
+        a.n_qt = (a.Sq + kPfBM - 1) / kPfBM;
+        a.n_kt = (a.Skv + kPfBN - 1) / kPfBN;
+        pl.n_planes = mask ? a.m_ne2 * a.m_ne3 : 0;
+        pl.ws_bytes = mask ? (size_t)pl.n_planes * a.n_qt * a.n_kt : 0;
+        a.n_splits = 1;
+        a.chunk = a.Skv;
+        return;
+    }
+    a.row_tiles = (a.M + 15) / 16;
+    const int64_t base = (int64_t)a.B * a.Nkv * a.row_tiles;
+    const int64_t max_splits = (a.Skv + kSplitKeyQuantum - 1) / kSplitKeyQuantum;
+    int64_t n_splits = 1;
+    if (base < kSplitTargetWgs) n_splits = std::min<int64_t>(max_splits, (kSplitTargetWgs + base - 1) / base);
+    int64_t chunk = (a.Skv + n_splits - 1) / n_splits;
+    chunk = (chunk + kSplitKeyQuantum - 1) / kSplitKeyQuantum * kSplitKeyQuantum;
+    n_splits = (a.Skv + chunk - 1) / chunk;
+    a.n_splits = (int32_t)n_splits;
+    a.chunk = (int32_t)chunk;
+    if (n_splits > 1) {
+        const size_t rows = (size_t)a.B * a.Nkv * a.M * n_splits;
+        pl.ws_bytes = rows * kD * sizeof(float) + rows * 2 * sizeof(float);
+    }
+}
+
+int ensure_workspace(size_t bytes, hipStream_t stream, void **out) {
+    *out = nullptr;
+    if (bytes == 0) return MXFA_OK;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(MXFA_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    if ((size_t)dev >= g_ws.size()) g_ws.resize(dev + 1);
+    Workspace &ws = g_ws[dev];
+    if (ws.size < bytes) {
+        if (ws.ptr) {
+            // queued kernels may still read the old buffer
+            e = hipStreamSynchronize(stream);
+            if (e != hipSuccess) return fail(MXFA_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+            (void)hipFree(ws.ptr);
+            ws.ptr = nullptr;
+            ws.size = 0;
+        }
+        size_t want = bytes + bytes / 4;
+        want = (want + 4095) & ~(size_t)4095;
+        e = hipMalloc(&ws.ptr, want);
+        if (e != hipSuccess) {
+            ws.ptr = nullptr;
+            return fail(MXFA_ERR_NOMEM, "hipMalloc(%zu): %s", want, hipGetErrorString(e));
+        }
+        ws.size = want;
+    }
+    *out = ws.ptr;
+    return MXFA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mxfa_supports(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
+                  const mxfa_params *params, const mxfa_tensor *dst) {
+    const int rc = check(q, k, v, mask, params, dst);
+    if (rc != MXFA_OK) return 0;
+    if (k->type == MXFA_TYPE_Q8_0) {
+        fail(MXFA_ERR_UNSUPPORTED, "Q8_0 K/V not built in this library");
+        return 0;
+    }
+    Plan pl;
+    make_plan(q, k, v, mask, params, nullptr, pl);
+    if (!pl.prefill && (int64_t)pl.args.Nkv * pl.args.row_tiles > 65535) {
+        fail(MXFA_ERR_UNSUPPORTED, "too many query rows per KV head for the split kernel");
+        return 0;
+    }
+    return 1;
+}
+
+int mxfa_flash_attn_ext(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
+                        const mxfa_params *params, mxfa_tensor *dst, void *hip_stream) {
+    if (!dst) return fail(MXFA_ERR_INVALID, "dst is required");
+    int rc = check(q, k, v, mask, params, dst);
+    if (rc != MXFA_OK) return rc;
+    if (k->type == MXFA_TYPE_Q8_0) return fail(MXFA_ERR_UNSUPPORTED, "Q8_0 K/V not built in this library");
+    hipStream_t stream = (hipStream_t)hip_stream;
+    Plan pl;
+    make_plan(q, k, v, mask, params, dst, pl);
+    void *ws = nullptr;
+    if (!pl.prefill && (int64_t)pl.args.Nkv * pl.args.row_tiles > 65535)
+        return fail(MXFA_ERR_UNSUPPORTED, "too many query rows per KV head for the split kernel");
+    rc = ensure_workspace(pl.ws_bytes, stream, &ws);
+    if (rc != MXFA_OK) return rc;
+    FaArgs &a = pl.args;
+    hipError_t e;
+    if (pl.prefill) {
+        if (a.mask) {
+            uint8_t *cls = (uint8_t *)ws;
+            a.tile_class = cls;
+            e = launch_mask_classify(a, pl.n_planes, cls, stream);
+            if (e != hipSuccess) return fail(MXFA_ERR_HIP, "mask classify launch: %s", hipGetErrorString(e));
+        }
+        e = launch_fa_prefill(a, pl.ktype, stream);
+        if (e != hipSuccess) return fail(MXFA_ERR_HIP, "prefill launch: %s", hipGetErrorString(e));
+        return MXFA_OK;
+    }
+    if (a.n_splits > 1) {
+        const size_t rows = (size_t)a.B * a.Nkv * a.M * a.n_splits;
+        a.part_o = (float *)ws;
+        a.part_ml = a.part_o + rows * kD;
+    }
+    e = launch_fa_split(a, pl.ktype, stream);
+    if (e != hipSuccess) return fail(MXFA_ERR_HIP, "split launch: %s", hipGetErrorString(e));
+    return MXFA_OK;
+}
+
+void mxfa_release(void) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    int cur = 0;
+    const bool have_cur = hipGetDevice(&cur) == hipSuccess;
+    for (size_t d = 0; d < g_ws.size(); d++) {
+        if (!g_ws[d].ptr) continue;
+        if (hipSetDevice((int)d) == hipSuccess) {
+            (void)hipDeviceSynchronize();
+            (void)hipFree(g_ws[d].ptr);
+        }
+        g_ws[d] = Workspace{};
+    }
+    if (have_cur) (void)hipSetDevice(cur);
+}
+
+const char *mxfa_status_string(int status) {
+    switch (status) {
+        case MXFA_OK: return "ok";
+        case MXFA_ERR_INVALID: return "invalid argument";
+        case MXFA_ERR_UNSUPPORTED: return "unsupported";
+        case MXFA_ERR_HIP: return "HIP error";
+        case MXFA_ERR_NOMEM: return "out of device memory";
+        default: return "unknown status";
+    }
+}
+
+const char *mxfa_last_error(void) { return g_last_error.c_str(); }
+
+int mxfa_version(void) { return 100; }
+
+}  // extern "C"

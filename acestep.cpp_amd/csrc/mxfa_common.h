@@ -1,0 +1,142 @@
+// mxfa_common.h -- shared device types and helpers for the gfx950 kernels.
+//
+// Layout conventions used by every kernel (ggml order, ne[0] innermost):
+//   q   F32  [D, Sq, Nh, B]   strided view (q_nb1..3)
+//   k,v F16/BF16 [D, Skv, Nkv, Bk] (k_nb1..3 / v_nb1..3), or Q8_0 blocks
+//   mask F16 [>=Skv, >=Sq, Nm2, Nm3] (m_nb1..3), broadcast by modulo
+//   dst F32 [D, Nh, Sq, B] contiguous
+// A "row" of the attention problem is one (query iq1, q head) pair; the
+// rows that share one KV head (GQA) are packed together into MFMA tiles.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mxfa {
+
+constexpr int kD = 128;                 // head size handled by the kernels
+constexpr float kLog2e = 1.4426950408889634f;
+
+enum : int { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_BF16 = 30 };
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Arguments shared by the attention kernels (passed by value).
+struct FaArgs {
+    const char *q, *k, *v, *mask;
+    float *dst;
+    int64_t q_nb1, q_nb2, q_nb3;
+    int64_t k_nb1, k_nb2, k_nb3;
+    int64_t v_nb1, v_nb2, v_nb3;
+    int64_t m_nb1, m_nb2, m_nb3;
+    int32_t m_ne2, m_ne3;
+    int32_t Sq, Nh, B, Skv, Nkv, G, rk3;  // G = Nh/Nkv, rk3 = B/Bk
+    int32_t M;                            // rows per (b, kv head) = Sq*G
+    int32_t row_tiles;                    // split kernel: ceil(M/16)
+    float scale, softcap;                 // softcap == 0: off
+    float max_bias, m0, m1;               // ALiBi (max_bias == 0: off)
+    uint32_t n_head_log2;
+    // split-KV
+    int32_t n_splits, chunk;
+    float *part_o, *part_ml;
+    // prefill: per (mask plane, q tile, k tile) class (see fa_mfma.hip)
+    const uint8_t *tile_class;
+    int32_t n_qt, n_kt;                   // tiles along Sq and Skv
+};
+
+// MFMA 16x16x32 for the two 16-bit float formats (8 k-values per lane).
+template <int T> struct Mfma16;
+template <> struct Mfma16<T_F16> {
+    typedef f16x8 v8;
+    static __device__ __forceinline__ f32x4 run(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint16_t from_f32(float x) {
+        return __builtin_bit_cast(uint16_t, (_Float16)x);
+    }
+};
+template <> struct Mfma16<T_BF16> {
+    typedef bf16x8 v8;
+    static __device__ __forceinline__ f32x4 run(v8 a, v8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint16_t from_f32(float x) {
+        return __builtin_bit_cast(uint16_t, (__bf16)x);
+    }
+};
+
+// MFMA 32x32x16 for the two 16-bit float formats (8 k-values per lane).
+template <int T> struct Mfma32;
+template <> struct Mfma32<T_F16> {
+    typedef f16x8 v8;
+    static __device__ __forceinline__ f32x16 run(v8 a, v8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct Mfma32<T_BF16> {
+    typedef bf16x8 v8;
+    static __device__ __forceinline__ f32x16 run(v8 a, v8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+__device__ __forceinline__ float h2f_bits(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Convert 8 floats to 8 16-bit values of format T (round to nearest even),
+// returned as the raw bits.
+template <int T>
+__device__ __forceinline__ u16x8 cvt8(f32x4 lo, f32x4 hi) {
+    u16x8 r;
+    r[0] = Mfma16<T>::from_f32(lo[0]);
+    r[1] = Mfma16<T>::from_f32(lo[1]);
+    r[2] = Mfma16<T>::from_f32(lo[2]);
+    r[3] = Mfma16<T>::from_f32(lo[3]);
+    r[4] = Mfma16<T>::from_f32(hi[0]);
+    r[5] = Mfma16<T>::from_f32(hi[1]);
+    r[6] = Mfma16<T>::from_f32(hi[2]);
+    r[7] = Mfma16<T>::from_f32(hi[3]);
+    return r;
+}
+
+// Sum of 8 16-bit values of format T (the rounded probabilities that feed
+// the PV product) with v_dot2 against (1, 1): the softmax denominator then
+// sums exactly the weights the numerator uses.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+template <int T>
+__device__ __forceinline__ float sum8(u16x8 p, float acc) {
+    const u32x4 w = __builtin_bit_cast(u32x4, p);
+    if constexpr (T == T_F16) {
+        const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w[i]), one, acc, false);
+    } else {
+        const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[i]), one, acc, false);
+    }
+    return acc;
+}
+
+// ALiBi slope of head h (ggml's formula; 1 when max_bias == 0).
+__device__ __forceinline__ float alibi_slope(const FaArgs &a, int h) {
+    if (a.max_bias <= 0.0f) return 1.0f;
+    const uint32_t hu = (uint32_t)h;
+    return hu < a.n_head_log2 ? powf(a.m0, (float)(hu + 1))
+                              : powf(a.m1, (float)(2 * (hu - a.n_head_log2) + 1));
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace mxfa

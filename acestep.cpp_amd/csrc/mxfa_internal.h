@@ -1,0 +1,28 @@
+// mxfa_internal.h -- launchers shared between the kernel translation units
+// and the host API (mxfa_api.cpp).  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "mxfa_common.h"
+
+namespace mxfa {
+
+// Split-KV kernel (+ combine pass when a.n_splits > 1).  ktype: T_F16/T_BF16.
+hipError_t launch_fa_split(const FaArgs &a, int ktype, hipStream_t stream);
+
+// Split-KV kernel over Q8_0 K/V (+ combine pass when a.n_splits > 1).
+hipError_t launch_fa_split_q8(const FaArgs &a, hipStream_t stream);
+
+// MFMA prefill kernel geometry.
+constexpr int kPfBM = 128;   // query rows per workgroup (4 waves x 32)
+constexpr int kPfBN = 64;    // keys per K/V tile
+
+// Mask tile classifier: writes a.tile_class[plane][qt][kt] for every
+// (mask plane, kPfBM-query tile, kPfBN-key tile).
+hipError_t launch_mask_classify(const FaArgs &a, int n_planes, uint8_t *classes, hipStream_t stream);
+
+// MFMA prefill / DiT kernel.  ktype: T_F16/T_BF16.
+hipError_t launch_fa_prefill(const FaArgs &a, int ktype, hipStream_t stream);
+
+}  // namespace mxfa

@@ -1,0 +1,186 @@
+"""Python binding of libmxfa (the gfx950 flash-attention engine, C ABI in
+include/mxfa.h).
+
+It mirrors the reference's operator interface for this path:
+``flash_attn_ext(q, k, v, mask, scale, max_bias, logit_softcap, prec)`` is
+ggml_flash_attn_ext + ggml_flash_attn_ext_set_prec as acestep.cpp calls them
+(src/qwen3-lm.h:465-469, :789-794; src/dit-graph.h:227-231, :348-352;
+src/qwen3-enc.h:195-199), and ``supports`` is the backend's supports_op for
+GGML_OP_FLASH_ATTN_EXT.  Tensors are ggml views: a type id, ne[4], nb[4] and
+a device pointer (`DeviceView`).  Device memory and streams come from torch
+(plumbing only); all arithmetic runs in the HIP kernels of libmxfa.so.
+
+The library must exist (built by ``make -C acestep.cpp_amd`` or
+``__graft_entry__.build()``); there is no fallback: importing this module
+without it raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from typing import Optional
+
+_PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_DIR, "lib", "libmxfa.so")
+
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_BF16 = 0, 1, 8, 30
+PREC_DEFAULT, PREC_F32 = 0, 10
+
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NOMEM = 0, -1, -2, -3, -4
+
+# Symbols declared in include/mxfa.h.
+EXPORTED_SYMBOLS = (
+    "mxfa_supports",
+    "mxfa_flash_attn_ext",
+    "mxfa_release",
+    "mxfa_status_string",
+    "mxfa_last_error",
+    "mxfa_version",
+)
+
+
+class MxfaTensor(ctypes.Structure):
+    _fields_ = [
+        ("type", ctypes.c_int32),
+        ("ne", ctypes.c_int64 * 4),
+        ("nb", ctypes.c_size_t * 4),
+        ("data", ctypes.c_void_p),
+    ]
+
+
+class MxfaParams(ctypes.Structure):
+    _fields_ = [
+        ("scale", ctypes.c_float),
+        ("max_bias", ctypes.c_float),
+        ("logit_softcap", ctypes.c_float),
+        ("prec", ctypes.c_int32),
+    ]
+
+
+class MxfaError(RuntimeError):
+    def __init__(self, status: int, detail: str):
+        super().__init__(f"mxfa status {status} ({status_string(status)}): {detail}")
+        self.status = status
+        self.detail = detail
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"libmxfa.so not built: {LIB_PATH} (run `make -C acestep.cpp_amd`)")
+    L = ctypes.CDLL(LIB_PATH)
+    P = ctypes.POINTER(MxfaTensor)
+    L.mxfa_supports.argtypes = [P, P, P, P, ctypes.POINTER(MxfaParams), P]
+    L.mxfa_supports.restype = ctypes.c_int
+    L.mxfa_flash_attn_ext.argtypes = [P, P, P, P, ctypes.POINTER(MxfaParams), P, ctypes.c_void_p]
+    L.mxfa_flash_attn_ext.restype = ctypes.c_int
+    L.mxfa_release.argtypes = []
+    L.mxfa_release.restype = None
+    L.mxfa_status_string.argtypes = [ctypes.c_int]
+    L.mxfa_status_string.restype = ctypes.c_char_p
+    L.mxfa_last_error.argtypes = []
+    L.mxfa_last_error.restype = ctypes.c_char_p
+    L.mxfa_version.argtypes = []
+    L.mxfa_version.restype = ctypes.c_int
+    return L
+
+
+lib = _load()
+
+
+def status_string(status: int) -> str:
+    return lib.mxfa_status_string(int(status)).decode()
+
+
+def last_error() -> str:
+    return lib.mxfa_last_error().decode()
+
+
+def version() -> int:
+    return int(lib.mxfa_version())
+
+
+@dataclass
+class DeviceView:
+    """A ggml-style tensor view over device memory."""
+
+    type: int
+    ne: tuple
+    nb: tuple
+    ptr: int                     # device address of element (0,0,0,0)
+    owner: object = None         # keeps the backing allocation alive
+
+    def desc(self) -> MxfaTensor:
+        t = MxfaTensor()
+        t.type = int(self.type)
+        for i in range(4):
+            t.ne[i] = int(self.ne[i])
+            t.nb[i] = int(self.nb[i])
+        t.data = ctypes.c_void_p(int(self.ptr)) if self.ptr else None
+        return t
+
+
+def _descs(q, k, v, mask, dst):
+    dq, dk, dv = q.desc(), k.desc(), v.desc()
+    dm = mask.desc() if mask is not None else None
+    dd = dst.desc() if dst is not None else None
+    ref = lambda d: ctypes.byref(d) if d is not None else None  # noqa: E731
+    return (dq, dk, dv, dm, dd), (ref(dq), ref(dk), ref(dv), ref(dm), ref(dd))
+
+
+def make_params(scale: float, max_bias: float = 0.0, logit_softcap: float = 0.0,
+                prec: int = PREC_F32) -> MxfaParams:
+    p = MxfaParams()
+    p.scale, p.max_bias, p.logit_softcap, p.prec = float(scale), float(max_bias), float(logit_softcap), int(prec)
+    return p
+
+
+def supports(q, k, v, mask, scale, max_bias=0.0, logit_softcap=0.0, prec=PREC_F32, dst=None) -> bool:
+    """supports_op: True when flash_attn_ext handles this combination."""
+    keep, refs = _descs(q, k, v, mask, dst)
+    p = make_params(scale, max_bias, logit_softcap, prec)
+    return bool(lib.mxfa_supports(refs[0], refs[1], refs[2], refs[3], ctypes.byref(p), refs[4]))
+
+
+def flash_attn_ext(q, k, v, mask, scale, max_bias=0.0, logit_softcap=0.0, prec=PREC_F32,
+                   dst: Optional[DeviceView] = None, stream: Optional[int] = None) -> DeviceView:
+    """GGML_OP_FLASH_ATTN_EXT on the GPU.  Returns the F32 [DV, Nh, Sq, B]
+    output view (allocated with torch when `dst` is None).  Asynchronous on
+    `stream` (default: torch's current stream).  Raises MxfaError on failure.
+    """
+    import torch
+
+    if dst is None:
+        DV, Nh, Sq, B = int(v.ne[0]), int(q.ne[2]), int(q.ne[1]), int(q.ne[3])
+        out = torch.empty((B, Sq, Nh, DV), dtype=torch.float32, device="cuda")
+        dst = DeviceView(TYPE_F32, (DV, Nh, Sq, B), (4, 4 * DV, 4 * DV * Nh, 4 * DV * Nh * Sq),
+                         out.data_ptr(), out)
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    keep, refs = _descs(q, k, v, mask, dst)
+    p = make_params(scale, max_bias, logit_softcap, prec)
+    rc = lib.mxfa_flash_attn_ext(refs[0], refs[1], refs[2], refs[3], ctypes.byref(p), refs[4],
+                                 ctypes.c_void_p(int(stream)))
+    if rc != OK:
+        raise MxfaError(rc, last_error())
+    return dst
+
+
+def release() -> None:
+    lib.mxfa_release()
+
+
+def upload(view, device="cuda") -> DeviceView:
+    """Copy a host view (any object with type/ne/nb/buf/offset) to the device,
+    keeping its strides: the whole backing buffer is copied."""
+    import numpy as np
+    import torch
+
+    buf = np.ascontiguousarray(view.buf).view(np.uint8).reshape(-1)
+    t = torch.from_numpy(buf).to(device)
+    return DeviceView(view.type, tuple(view.ne), tuple(view.nb), t.data_ptr() + int(view.offset), t)
+
+
+def output_tensor(dst: DeviceView):
+    """The torch tensor [B, Sq, Nh, DV] behind an output view."""
+    return dst.owner

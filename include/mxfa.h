@@ -1,0 +1,117 @@
+/*
+ * mxfa.h -- MI355X (gfx950) flash-attention engine, C ABI.
+ *
+ * The engine implements ggml's GGML_OP_FLASH_ATTN_EXT so that acestep.cpp's
+ * attention graphs run unchanged on top of it.  The reference builds every
+ * attention node as
+ *
+ *     attn = ggml_flash_attn_ext(ctx, q, k, v, mask, scale, max_bias, softcap);
+ *     ggml_flash_attn_ext_set_prec(attn, GGML_PREC_F32);
+ *
+ * at src/qwen3-lm.h:465-469 (LM prefill / single decode), :789-794 (batched
+ * CFG decode), src/dit-graph.h:227-231 (DiT self-attention), :348-352 (DiT
+ * cross-attention) and src/qwen3-enc.h:195-199 (text / lyric / timbre
+ * encoders).  The node is executed by whatever ggml backend owns it
+ * (src/backend.h:90-145, src/static-graph.h:54-58).  A ggml backend's
+ * graph_compute maps such a node onto mxfa_flash_attn_ext() below (see
+ * include/mxfa_ggml.h for the header-only adapter from struct ggml_tensor),
+ * and its supports_op maps onto mxfa_supports().
+ *
+ * All tensors are owned by the caller and live in device memory (the ggml
+ * backend buffer).  Descriptors carry ggml's own fields: type id, ne[4]
+ * (element counts, ne[0] innermost) and nb[4] (byte strides).
+ *
+ *   q    : F32            [DK, Sq,  Nh,  B ]  any strides, nb[0] = 4
+ *   k    : F16|BF16|Q8_0  [DK, Skv, Nkv, Bk]  rows contiguous (nb[0] = type size)
+ *   v    : same type as k [DV, Skv, Nkv, Bk]
+ *   mask : F16 or NULL    [>=Skv, >=Sq, Nm2, Nm3], additive, broadcast over
+ *                         heads (iq2 % Nm2) and batches (iq3 % Nm3);
+ *                         -inf entries exclude the key entirely
+ *   dst  : F32 contiguous [DV, Nh, Sq, B]   (ggml's permuted FA output)
+ *
+ * with GQA head map kv_head = q_head / (Nh / Nkv) and batch broadcast
+ * kv_batch = b / (B / Bk).  Semantics are those of ggml's CPU kernel
+ * (softmax(scale * K.Q [+softcap] + slope * mask) . V, a row with no
+ * unmasked key gives 0); accumulation is fp32 throughout.
+ */
+#ifndef MXFA_H
+#define MXFA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (enum ggml_type values; they are stable in the GGUF format). */
+#define MXFA_TYPE_F32  0
+#define MXFA_TYPE_F16  1
+#define MXFA_TYPE_Q8_0 8
+#define MXFA_TYPE_BF16 30
+
+/* ggml_prec values (GGML_PREC_DEFAULT / GGML_PREC_F32).  The engine always
+ * accumulates in fp32, so both are accepted and treated alike. */
+#define MXFA_PREC_DEFAULT 0
+#define MXFA_PREC_F32     10
+
+/* Status codes: 0 = success, negative = failure; never exit()/abort(). */
+#define MXFA_OK               0
+#define MXFA_ERR_INVALID     -1   /* malformed descriptor / NULL pointer      */
+#define MXFA_ERR_UNSUPPORTED -2   /* valid op, shape/type not handled here    */
+#define MXFA_ERR_HIP         -3   /* HIP runtime error (launch, device)       */
+#define MXFA_ERR_NOMEM       -4   /* workspace allocation failed              */
+
+/* One tensor, as ggml describes it (struct ggml_tensor: type, ne, nb, data). */
+typedef struct mxfa_tensor {
+    int32_t type;
+    int64_t ne[4];
+    size_t  nb[4];
+    void   *data;
+} mxfa_tensor;
+
+/* The op parameters of GGML_OP_FLASH_ATTN_EXT: op_params float[0..2] =
+ * scale, max_bias, logit_softcap and int32[3] = prec. */
+typedef struct mxfa_params {
+    float   scale;
+    float   max_bias;
+    float   logit_softcap;
+    int32_t prec;
+} mxfa_params;
+
+/* supports_op for GGML_OP_FLASH_ATTN_EXT: returns 1 when
+ * mxfa_flash_attn_ext() handles this combination, 0 otherwise (the ggml
+ * scheduler then places the node on another backend, as
+ * src/static-graph.h:12-19 and :31-52 expect).  Reads descriptors only;
+ * no device access.  `dst` may be NULL (then its layout is not checked). */
+int mxfa_supports(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
+                  const mxfa_tensor *mask, const mxfa_params *params, const mxfa_tensor *dst);
+
+/* Execute GGML_OP_FLASH_ATTN_EXT on the current HIP device, ordered on
+ * `hip_stream` (a hipStream_t; NULL = the default stream).  Asynchronous:
+ * returns after the launches are queued.  The engine owns only a
+ * device workspace for split-KV partials and mask tile classes; it is grown
+ * on demand (a grow makes the call synchronise the stream once) and kept
+ * until mxfa_release().  Calls on different streams of one device must not
+ * overlap in time (they share that workspace).  Returns MXFA_OK or a
+ * negative status; on failure nothing was launched. */
+int mxfa_flash_attn_ext(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
+                        const mxfa_tensor *mask, const mxfa_params *params, mxfa_tensor *dst,
+                        void *hip_stream);
+
+/* Free the workspaces of every device (synchronises each device first). */
+void mxfa_release(void);
+
+/* Human-readable text for a status code; last error detail for MXFA_ERR_HIP
+ * and MXFA_ERR_UNSUPPORTED (thread-local). */
+const char *mxfa_status_string(int status);
+const char *mxfa_last_error(void);
+
+/* Library version: major*10000 + minor*100 + patch. */
+int mxfa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXFA_H */

@@ -1,0 +1,281 @@
+"""GPU parity: libmxfa's HIP kernels against the CPU oracle.
+
+Every case is called through the C ABI (mxfa.flash_attn_ext ->
+mxfa_flash_attn_ext) on device copies of host inputs, and compared on the
+same bytes with three references:
+
+  gate   ggml's CPU flash_attn_ext algorithm with an fp32 accumulator
+         (oracle fa_ggml(acc_f32=True)): max-abs <= 2e-3 and per-row
+         cosine >= 0.9999 (bf16 inputs: max-abs <= 1e-2, since P is rounded
+         to bf16 for the MFMA);
+  exact  fp64 two-pass softmax on the same rounded Q (reported; asserted
+         at the same bar);
+  strict ggml's CPU kernel as it runs (fp16 running accumulator for F16 V).
+         Its own distance to exact maths exceeds the bar on long F16 rows,
+         so it is asserted through the triangle: the GPU may be no further
+         from strict ggml than exact maths is, plus 1e-3 / 1e-5 in cosine.
+"""
+from __future__ import annotations
+
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import MAX_ABS_TOL, ROW_COS_TOL, row_metrics
+
+pytestmark = pytest.mark.gpu
+
+
+def _need_gpu():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+@pytest.fixture(scope="module")
+def mx():
+    _need_gpu()
+    import mxfa
+
+    return mxfa
+
+
+def run_gpu(mx, case):
+    import torch
+
+    dq = mx.upload(case.q)
+    dk = mx.upload(case.k)
+    dv = mx.upload(case.v)
+    dm = mx.upload(case.mask) if case.mask is not None else None
+    out = mx.flash_attn_ext(dq, dk, dv, dm, case.scale, case.max_bias, case.softcap)
+    torch.cuda.synchronize()
+    return mx.output_tensor(out).cpu().numpy()
+
+
+def check(mx, case, label, bf16=False, exact=True, strict=True, n_threads=None):
+    import oracle
+
+    print(f"[parity] {label}: q{tuple(case.q.ne)} k{tuple(case.k.ne)} t{case.k.type} "
+          f"mask={'none' if case.mask is None else tuple(case.mask.ne)}", flush=True)
+    got = run_gpu(mx, case)
+    assert got.shape == case.out_shape
+    assert not np.isnan(got).any()
+    gate = oracle.fa_ggml(case.q, case.k, case.v, case.mask, case.scale, case.max_bias, case.softcap,
+                          n_threads=n_threads, acc_f32=True)
+    mg = row_metrics(got, gate)
+    tol = 1e-2 if bf16 else MAX_ABS_TOL
+    res = {"gate": mg}
+    if exact:
+        ex = oracle.fa_exact(case.q, case.k, case.v, case.mask, case.scale, case.max_bias, case.softcap,
+                             q_round=True, n_threads=n_threads)
+        res["exact"] = row_metrics(got, ex)
+    if strict:
+        st = oracle.fa_ggml(case.q, case.k, case.v, case.mask, case.scale, case.max_bias, case.softcap,
+                            n_threads=n_threads)
+        res["strict"] = row_metrics(got, st)
+        if exact:
+            res["strict_vs_exact"] = row_metrics(st, ex)
+    print(f"[parity] {label}: " + " | ".join(
+        f"{k} max_abs={v['max_abs']:.3e} min_cos={v['min_cos']:.7f}" for k, v in res.items()), flush=True)
+    assert mg["max_abs"] <= tol and mg["min_cos"] >= ROW_COS_TOL, (label, mg)
+    if exact:
+        assert res["exact"]["max_abs"] <= tol and res["exact"]["min_cos"] >= ROW_COS_TOL, (label, res["exact"])
+    if strict and exact:
+        sv = res["strict_vs_exact"]
+        assert res["strict"]["max_abs"] <= sv["max_abs"] + 1e-3, (label, res)
+        assert res["strict"]["min_cos"] >= sv["min_cos"] - 1e-5, (label, res)
+    return got, res
+
+
+# ---------------------------------------------------------------------------
+# the five benchmark configurations, full size
+# ---------------------------------------------------------------------------
+
+def test_c1_decode_06b(mx):
+    from mxfa import cases
+
+    check(mx, cases.c1(), "C1 decode mask")
+    check(mx, cases.c1(mask_mode="none"), "C1 decode no-mask")
+
+
+def test_c1_mask_and_null_agree(mx):
+    from mxfa import cases
+
+    a = run_gpu(mx, cases.c1())
+    b = run_gpu(mx, cases.c1(mask_mode="none"))
+    assert np.array_equal(a, b)
+
+
+def test_c2_causal_prefill_4b(mx):
+    from mxfa import cases
+
+    check(mx, cases.c2(), "C2 prefill 2048")
+
+
+def test_c3_cfg_decode_4b(mx):
+    from mxfa import cases
+
+    c = cases.c3()
+    print("[parity] C3 lengths", c.meta["lengths"], "n_kv_pad", c.meta["n_kv_pad"], flush=True)
+    check(mx, c, "C3 cfg decode")
+
+
+def test_c4_dit_self(mx):
+    from mxfa import cases
+
+    # gate at full size; exact / strict on a 1024-token slice of the shape
+    check(mx, cases.c4_self(), "C4 self 3000 (gate)", exact=False, strict=False)
+    check(mx, cases.c4_self(S=1024), "C4 self 1024")
+    check(mx, cases.c4_self(Nkv=8, S=1024), "C4 self 1024 GQA 16/8")
+
+
+def test_c4_dit_cross(mx):
+    from mxfa import cases
+
+    c = cases.c4_cross()
+    print("[parity] C4x pads", c.meta["pads"], flush=True)
+    check(mx, c, "C4 cross")
+    check(mx, cases.c4_cross(Nkv=8), "C4 cross GQA 16/8")
+
+
+def test_c5_q8_0_decode(mx):
+    from mxfa import cases
+
+    c = cases.c5()
+    dq, dk, dv = mx.upload(c.q), mx.upload(c.k), mx.upload(c.v)
+    dm = mx.upload(c.mask)
+    if not mx.supports(dq, dk, dv, dm, c.scale):
+        pytest.skip("Q8_0 K/V kernel not in this build: " + mx.last_error())
+    check(mx, c, "C5 q8_0 decode")
+
+
+# ---------------------------------------------------------------------------
+# edge cases (both kernels)
+# ---------------------------------------------------------------------------
+
+def _rand_case(seed, B=2, Bk=None, Sq=5, Nh=8, Nkv=2, Skv=300, kv_type=1, mask="random",
+               mask_heads=1, softcap=0.0, max_bias=0.0, q_layout="perm", p_masked=0.3):
+    from mxfa.cases import FaCase, HostView, to_f16_bits, to_bf16_bits
+
+    rng = np.random.default_rng(seed)
+    Bk = B if Bk is None else Bk
+    D = 128
+    qa = rng.standard_normal((B, Nh, Sq, D)).astype(np.float32)
+    if q_layout == "perm":
+        mem = np.ascontiguousarray(qa.transpose(0, 2, 1, 3))
+        q = HostView(0, (D, Sq, Nh, B), (4, Nh * D * 4, D * 4, Nh * D * Sq * 4), mem.reshape(-1))
+    else:
+        q = HostView(0, (D, Sq, Nh, B), (4, D * 4, D * Sq * 4, D * Sq * Nh * 4), qa.reshape(-1))
+    conv = to_bf16_bits if kv_type == 30 else to_f16_bits
+    ka = conv(rng.standard_normal((Bk, Nkv, Skv, D)).astype(np.float32)).reshape(-1)
+    va = conv(rng.standard_normal((Bk, Nkv, Skv, D)).astype(np.float32)).reshape(-1)
+    nb = (2, 2 * D, 2 * D * Skv, 2 * D * Skv * Nkv)
+    k = HostView(kv_type, (D, Skv, Nkv, Bk), nb, ka)
+    v = HostView(kv_type, (D, Skv, Nkv, Bk), nb, va)
+    m = None
+    if mask is not None:
+        Hm = mask_heads
+        if mask == "random":
+            allowed = rng.random((B, Hm, Sq, Skv)) > p_masked
+            vals = np.where(allowed, rng.standard_normal((B, Hm, Sq, Skv)) * 0.5, -np.inf)
+        elif mask == "causal":
+            allowed = np.arange(Skv)[None, :] <= (Skv - Sq + np.arange(Sq))[:, None]
+            vals = np.broadcast_to(np.where(allowed, 0.0, -np.inf), (B, Hm, Sq, Skv))
+        vals = np.asarray(vals, dtype=np.float32)
+        if max_bias > 0:
+            vals = np.where(np.isneginf(vals), vals, -np.abs(vals) * 3).astype(np.float32)
+        bits = vals.astype(np.float16).view(np.uint16).reshape(-1)
+        m = HostView(1, (Skv, Sq, Hm, B), (2, 2 * Skv, 2 * Skv * Sq, 2 * Skv * Sq * Hm), bits)
+    return FaCase(f"rand{seed}", q, k, v, m, 1.0 / math.sqrt(D), max_bias=max_bias, softcap=softcap)
+
+
+@pytest.mark.parametrize("Sq", [1, 5, 16, 63, 64, 200])
+def test_ragged_shapes_and_random_masks(mx, Sq):
+    # Sq < 64 runs the split-KV kernel, Sq >= 64 the MFMA prefill kernel
+    c = _rand_case(100 + Sq, B=2, Sq=Sq, Nh=8, Nkv=2, Skv=333)
+    check(mx, c, f"random mask Sq={Sq} Skv=333")
+
+
+def test_fully_masked_rows_are_zero(mx):
+    for Sq in (3, 130):
+        c = _rand_case(7 + Sq, B=1, Sq=Sq, Nh=4, Nkv=4, Skv=200)
+        bits = c.mask.buf.reshape(1, 1, Sq, 200)
+        bits[0, 0, 1, :] = 0xFC00
+        bits[0, 0, Sq - 1, :] = 0xFC00
+        got, _ = check(mx, c, f"fully masked rows Sq={Sq}")
+        assert np.all(got[0, 1] == 0.0) and np.all(got[0, Sq - 1] == 0.0)
+
+
+def test_masked_tail_with_nan_does_not_leak(mx):
+    """The reference zeroes its KV cache so masked tail slots are finite
+    (src/qwen3-lm.h:255-258).  The split kernel must not depend on that:
+    NaN in slots masked for every row never reaches the output."""
+    from mxfa import cases
+
+    c = cases.lm_batch("nan", N=2, Nh=8, Nkv=2, max_seq=1024, lengths=[300, 700])
+    for buf in (c.k.buf, c.v.buf):
+        view = buf.reshape(2, 2, 1024, 128)
+        view[0, :, 300:, :] = 0x7E00      # fp16 NaN beyond the valid length
+        view[1, :, 700:, :] = 0x7E00
+    check(mx, c, "nan tail decode")
+
+
+def test_gqa_batch_and_head_broadcast(mx):
+    # KV batch broadcast (Bk = 1 for B = 4), GQA 8:1, mask per head
+    c = _rand_case(31, B=4, Bk=1, Sq=3, Nh=8, Nkv=1, Skv=257, mask_heads=8)
+    check(mx, c, "bk broadcast + per-head mask (split)")
+    c = _rand_case(32, B=2, Bk=1, Sq=150, Nh=4, Nkv=2, Skv=190, mask_heads=4)
+    check(mx, c, "bk broadcast + per-head mask (prefill)")
+
+
+def test_contiguous_q_and_no_mask(mx):
+    for Sq in (2, 129):
+        c = _rand_case(40 + Sq, B=1, Sq=Sq, Nh=4, Nkv=4, Skv=517, mask=None, q_layout="contig")
+        check(mx, c, f"no mask contiguous q Sq={Sq}")
+
+
+def test_softcap_and_alibi(mx):
+    for Sq in (4, 100):
+        c = _rand_case(50 + Sq, B=1, Sq=Sq, Nh=16, Nkv=4, Skv=129, softcap=30.0)
+        check(mx, c, f"softcap Sq={Sq}")
+        c = _rand_case(60 + Sq, B=1, Sq=Sq, Nh=16, Nkv=4, Skv=129, max_bias=8.0)
+        check(mx, c, f"alibi Sq={Sq}")
+
+
+def test_bf16_kv(mx):
+    for Sq in (1, 96):
+        c = _rand_case(70 + Sq, B=2, Sq=Sq, Nh=8, Nkv=4, Skv=211, kv_type=30)
+        check(mx, c, f"bf16 Sq={Sq}", bf16=True)
+
+
+def test_causal_prefill_offsets(mx):
+    # prompt continuation: Sq new tokens at the end of a longer window
+    c = _rand_case(80, B=1, Sq=300, Nh=8, Nkv=2, Skv=1000, mask="causal")
+    check(mx, c, "causal continuation 300 of 1000")
+
+
+def test_workspace_grows_and_repeats(mx):
+    from mxfa import cases
+
+    small = cases.lm_batch("ws", N=2, Nh=8, Nkv=2, max_seq=512, lengths=[100, 512])
+    big = cases.lm_batch("ws", N=8, Nh=32, Nkv=8, max_seq=4096, lmin=1000, lmax=4096)
+    a1 = run_gpu(mx, small)
+    run_gpu(mx, big)
+    a2 = run_gpu(mx, small)
+    assert np.array_equal(a1, a2)
+    check(mx, big, "after growth")
+
+
+def test_invalid_arguments_raise(mx):
+    from mxfa import cases
+
+    c = cases.c1()
+    dq, dk, dv = mx.upload(c.q), mx.upload(c.k), mx.upload(c.v)
+    bad = mx.DeviceView(dk.type, (64,) + tuple(dk.ne[1:]), dk.nb, dk.ptr, dk.owner)
+    with pytest.raises(mx.MxfaError):
+        mx.flash_attn_ext(dq, bad, dv, None, c.scale)
+    assert not mx.supports(dq, bad, dv, None, c.scale)
