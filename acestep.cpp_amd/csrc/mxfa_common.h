@@ -119,12 +119,17 @@ __device__ __forceinline__ float sum8(u16x8 p, float acc) {
     if constexpr (T == T_F16) {
         const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w[i]), one, acc, false);
+        for (int i = 0; i < 4; i++) {
+            const uint32_t wi = w[i];   // bit_cast of a vector element lvalue reads element 0
+            acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, wi), one, acc, false);
+        }
     } else {
         const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[i]), one, acc, false);
+        for (int i = 0; i < 4; i++) {
+            const uint32_t wi = w[i];
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wi), one, acc, false);
+        }
     }
     return acc;
 }
