@@ -315,15 +315,19 @@ __global__ void __launch_bounds__(128) fa_combine_kernel(const FaArgs a) {
 }
 
 hipError_t launch_fa_split(const FaArgs &a, int ktype, hipStream_t stream) {
-    dim3 grid(a.n_splits, a.Nkv * a.row_tiles, a.B);
-    if (ktype == T_F16) hipLaunchKernelGGL(fa_split_kernel<T_F16>, grid, dim3(256), 0, stream, a);
-    else if (ktype == T_BF16) hipLaunchKernelGGL(fa_split_kernel<T_BF16>, grid, dim3(256), 0, stream, a);
-    else return hipErrorInvalidValue;
-    hipError_t e = hipGetLastError();
+    if (ktype != T_F16 && ktype != T_BF16) return hipErrorInvalidValue;
+    const dim3 grid(a.n_splits, a.Nkv * a.row_tiles, a.B);
+    hipError_t e = timed_launch("fa_split", stream, [&] {
+        if (ktype == T_F16) hipLaunchKernelGGL(fa_split_kernel<T_F16>, grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL(fa_split_kernel<T_BF16>, grid, dim3(256), 0, stream, a);
+        return hipGetLastError();
+    });
     if (e != hipSuccess || a.n_splits == 1) return e;
     const int64_t rows = (int64_t)a.B * a.Nkv * a.M;
-    hipLaunchKernelGGL(fa_combine_kernel, dim3((unsigned)rows), dim3(128), 0, stream, a);
-    return hipGetLastError();
+    return timed_launch("fa_combine", stream, [&] {
+        hipLaunchKernelGGL(fa_combine_kernel, dim3((unsigned)rows), dim3(128), 0, stream, a);
+        return hipGetLastError();
+    });
 }
 
 }  // namespace mxfa

@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -237,7 +238,74 @@ int ensure_workspace(size_t bytes, hipStream_t stream, void **out) {
     return MXFA_OK;
 }
 
+// -- per-kernel timing ---------------------------------------------------------
+struct TimedLaunch {
+    std::string family;
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+struct FamilyStats {
+    double ms = 0.0;
+    int64_t launches = 0;
+};
+std::atomic<bool> g_timing{false};
+std::mutex g_timing_mu;
+std::vector<TimedLaunch *> g_pending;
+std::vector<std::pair<std::string, FamilyStats>> g_stats;
+
+FamilyStats &stats_of(const std::string &f) {
+    for (auto &kv : g_stats)
+        if (kv.first == f) return kv.second;
+    g_stats.emplace_back(f, FamilyStats{});
+    return g_stats.back().second;
+}
+
+// Waits for and folds every pending event pair into the per-family totals.
+void drain_pending() {
+    for (TimedLaunch *t : g_pending) {
+        float ms = 0.0f;
+        if (t->stop && hipEventSynchronize(t->stop) == hipSuccess &&
+            hipEventElapsedTime(&ms, t->start, t->stop) == hipSuccess) {
+            FamilyStats &st = stats_of(t->family);
+            st.ms += ms;
+            st.launches += 1;
+        }
+        if (t->start) (void)hipEventDestroy(t->start);
+        if (t->stop) (void)hipEventDestroy(t->stop);
+        delete t;
+    }
+    g_pending.clear();
+}
+
 }  // namespace
+
+namespace mxfa {
+
+bool timing_enabled() { return g_timing.load(std::memory_order_relaxed); }
+
+void timing_begin(const char *family, hipStream_t stream, void **token) {
+    TimedLaunch *t = new TimedLaunch;
+    t->family = family;
+    if (hipEventCreate(&t->start) != hipSuccess || hipEventRecord(t->start, stream) != hipSuccess) {
+        if (t->start) (void)hipEventDestroy(t->start);
+        delete t;
+        *token = nullptr;
+        return;
+    }
+    *token = t;
+}
+
+void timing_end(void *token, hipStream_t stream) {
+    TimedLaunch *t = (TimedLaunch *)token;
+    if (!t) return;
+    if (hipEventCreate(&t->stop) != hipSuccess || hipEventRecord(t->stop, stream) != hipSuccess) {
+        if (t->stop) (void)hipEventDestroy(t->stop);
+        t->stop = nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    g_pending.push_back(t);
+}
+
+}  // namespace mxfa
 
 extern "C" {
 
@@ -278,10 +346,11 @@ int mxfa_flash_attn_ext(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_t
         if (a.mask) {
             uint8_t *cls = (uint8_t *)ws;
             a.tile_class = cls;
-            e = launch_mask_classify(a, pl.n_planes, cls, stream);
+            e = timed_launch("mask_classify", stream,
+                             [&] { return launch_mask_classify(a, pl.n_planes, cls, stream); });
             if (e != hipSuccess) return fail(MXFA_ERR_HIP, "mask classify launch: %s", hipGetErrorString(e));
         }
-        e = launch_fa_prefill(a, pl.ktype, stream);
+        e = timed_launch("fa_prefill", stream, [&] { return launch_fa_prefill(a, pl.ktype, stream); });
         if (e != hipSuccess) return fail(MXFA_ERR_HIP, "prefill launch: %s", hipGetErrorString(e));
         return MXFA_OK;
     }
@@ -322,6 +391,24 @@ const char *mxfa_status_string(int status) {
 }
 
 const char *mxfa_last_error(void) { return g_last_error.c_str(); }
+
+void mxfa_timing_enable(int on) { g_timing.store(on != 0); }
+
+int mxfa_timing_read(const char *kernel, double *total_ms, int64_t *launches) {
+    if (!kernel || !total_ms || !launches) return fail(MXFA_ERR_INVALID, "NULL argument");
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    drain_pending();
+    const FamilyStats &st = stats_of(kernel);
+    *total_ms = st.ms;
+    *launches = st.launches;
+    return MXFA_OK;
+}
+
+void mxfa_timing_reset(void) {
+    std::lock_guard<std::mutex> lock(g_timing_mu);
+    drain_pending();
+    g_stats.clear();
+}
 
 int mxfa_version(void) { return 100; }
 

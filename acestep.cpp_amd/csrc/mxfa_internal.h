@@ -25,4 +25,20 @@ hipError_t launch_mask_classify(const FaArgs &a, int n_planes, uint8_t *classes,
 // MFMA prefill / DiT kernel.  ktype: T_F16/T_BF16.
 hipError_t launch_fa_prefill(const FaArgs &a, int ktype, hipStream_t stream);
 
+// Per-kernel timing: when enabled, timed_launch() brackets `launch` with
+// two events on `stream` and files them under `family`.
+bool timing_enabled();
+void timing_begin(const char *family, hipStream_t stream, void **token);
+void timing_end(void *token, hipStream_t stream);
+
+template <typename F>
+hipError_t timed_launch(const char *family, hipStream_t stream, F launch) {
+    if (!timing_enabled()) return launch();
+    void *tok = nullptr;
+    timing_begin(family, stream, &tok);
+    const hipError_t e = launch();
+    timing_end(tok, stream);
+    return e;
+}
+
 }  // namespace mxfa

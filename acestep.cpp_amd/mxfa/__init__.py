@@ -37,6 +37,9 @@ EXPORTED_SYMBOLS = (
     "mxfa_status_string",
     "mxfa_last_error",
     "mxfa_version",
+    "mxfa_timing_enable",
+    "mxfa_timing_read",
+    "mxfa_timing_reset",
 )
 
 
@@ -82,6 +85,13 @@ def _load():
     L.mxfa_last_error.restype = ctypes.c_char_p
     L.mxfa_version.argtypes = []
     L.mxfa_version.restype = ctypes.c_int
+    L.mxfa_timing_enable.argtypes = [ctypes.c_int]
+    L.mxfa_timing_enable.restype = None
+    L.mxfa_timing_read.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
+                                   ctypes.POINTER(ctypes.c_int64)]
+    L.mxfa_timing_read.restype = ctypes.c_int
+    L.mxfa_timing_reset.argtypes = []
+    L.mxfa_timing_reset.restype = None
     return L
 
 
@@ -168,6 +178,25 @@ def flash_attn_ext(q, k, v, mask, scale, max_bias=0.0, logit_softcap=0.0, prec=P
 
 def release() -> None:
     lib.mxfa_release()
+
+
+def timing_enable(on: bool = True) -> None:
+    """Bracket every engine kernel launch with HIP events (profiling aid)."""
+    lib.mxfa_timing_enable(int(bool(on)))
+
+
+def timing_read(kernel: str):
+    """(total_ms, launches) of one kernel family since the last reset."""
+    ms = ctypes.c_double(0.0)
+    n = ctypes.c_int64(0)
+    rc = lib.mxfa_timing_read(kernel.encode(), ctypes.byref(ms), ctypes.byref(n))
+    if rc != OK:
+        raise MxfaError(rc, last_error())
+    return ms.value, n.value
+
+
+def timing_reset() -> None:
+    lib.mxfa_timing_reset()
 
 
 def upload(view, device="cuda") -> DeviceView:

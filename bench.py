@@ -1,0 +1,255 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X flash-attention engine (GGML_OP_FLASH_ATTN_EXT).
+
+Headline workload (the config the metric is quoted
+on): Qwen3-4B-shaped causal prefill attention, B=1, 2048 tokens, 32 Q / 8 KV
+heads, D=128, F32 Q, F16 K/V in a 2048-slot cache, F16 causal mask.  One
+"step" = one mxfa_flash_attn_ext call on inputs already resident in HBM.
+
+    value     = algorithmic TFLOP/s of the op (4*D per unmasked (q, k) pair
+                per q head, causal: 34.38 GFLOP) over the timed steps;
+    roofline  = the dominant kernel (fa_prefill), achieved = its algorithmic
+                FLOPs / its average duration, timed live with HIP events on
+                its launch stream (mxfa_timing_*), against the fp16 dense MFMA
+                peak (2.5 PFLOP/s); traffic = HBM bytes per launch from the
+                committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary if present;
+    cpu_baseline = the ggml-CPU-semantics oracle (strict: fp16 V accumulator)
+                timed on this host on the full workload.
+
+The other configurations (C1, C3, C4 self/cross, C5) are reported under
+"configs" with their own bound (TFLOP/s vs MFMA peak, or KV GB/s vs the 8 TB/s
+HBM peak).  Inputs of bandwidth-bound configs are rotated over enough device
+copies that consecutive steps do not hit in the 256 MB Infinity Cache.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2,c3] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(REPO, "acestep.cpp_amd"),):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "FA TFLOP/s (prefill/DiT) + decode KV GB/s, % of MI355X roofline, 1 GPU"
+PEAK_TFLOPS = 2500.0     # MI355X dense fp16/bf16 MFMA
+PEAK_GBS = 8000.0        # MI355X HBM3E
+ROTATE_BYTES = 600e6     # > 256 MB Infinity Cache
+
+DESCR = {
+    "c1": "Qwen3-0.6B decode: B=1, 1 token, 16/8 heads, D=128, KV 512 (F16 cache view, zero mask)",
+    "c2": "Qwen3-4B causal prefill: B=1, 2048 tokens, 32/8 heads, D=128, F16 KV, F16 causal mask",
+    "c3": "Qwen3-4B batched CFG decode: 8 seqs, 32/8 heads, D=128, F16 cache cap 8192, lengths U[1024,8192]",
+    "c4s": "DiT self-attention: B=2 (CFG), 3000 tokens, 16/16 heads, D=128, F16 KV, no mask",
+    "c4x": "DiT cross-attention: B=2, 3000 q x 256 keys, 16/16 heads, D=128, F16 KV, padding mask 0-128",
+    "c5": "Qwen3-4B decode over Q8_0 KV: B=4, 32/8 heads, D=128, KV 8192",
+}
+BOUND = {"c1": "hbm", "c2": "mfma", "c3": "hbm", "c4s": "mfma", "c4x": "hbm", "c5": "hbm"}
+KERNEL = {"c1": "fa_split", "c2": "fa_prefill", "c3": "fa_split", "c4s": "fa_prefill", "c4x": "fa_prefill",
+          "c5": "fa_split"}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def upload_copies(mx, case, n):
+    copies = []
+    for _ in range(n):
+        d = dict(q=mx.upload(case.q), k=mx.upload(case.k), v=mx.upload(case.v),
+                 m=mx.upload(case.mask) if case.mask is not None else None)
+        copies.append(d)
+    return copies
+
+
+def time_case(mx, torch, case, steps, warmup, rotate_bytes=None):
+    """Returns (ms per call, per-kernel avg ms dict)."""
+    from mxfa import cases as C
+
+    w = C.work(case)
+    per_iter = w["bytes"]
+    n_copies = 1 if rotate_bytes is None else int(min(16, max(1, math.ceil(rotate_bytes / max(per_iter, 1)))))
+    copies = upload_copies(mx, case, n_copies)
+    outs = []
+    for _ in range(n_copies):
+        B, Sq, Nh, DV = case.out_shape
+        o = torch.empty((B, Sq, Nh, DV), dtype=torch.float32, device="cuda")
+        outs.append(mx.DeviceView(0, (DV, Nh, Sq, B), (4, 4 * DV, 4 * DV * Nh, 4 * DV * Nh * Sq),
+                                  o.data_ptr(), o))
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step(i):
+        c = copies[i % n_copies]
+        mx.flash_attn_ext(c["q"], c["k"], c["v"], c["m"], case.scale, case.max_bias, case.softcap,
+                          dst=outs[i % n_copies], stream=stream)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(steps):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    # per-kernel durations, HIP events on the launch stream
+    mx.timing_reset()
+    mx.timing_enable(True)
+    for i in range(steps):
+        step(i)
+    torch.cuda.synchronize()
+    mx.timing_enable(False)
+    kern = {}
+    for fam in ("fa_prefill", "mask_classify", "fa_split", "fa_combine"):
+        tot, n = mx.timing_read(fam)
+        if n:
+            kern[fam] = tot / n
+    mx.timing_reset()
+    del copies, outs
+    torch.cuda.empty_cache()
+    return ms, kern, w, n_copies
+
+
+def summarize(name, ms, kern, w, n_copies):
+    bound = BOUND[name]
+    kname = KERNEL[name]
+    kms = kern.get(kname)
+    out = dict(workload=DESCR[name], ms=round(ms, 5), kernels_ms={k: round(v, 5) for k, v in kern.items()},
+               flops=w["flops"], kv_bytes=w["kv_bytes"], bytes=w["bytes"], copies=n_copies)
+    out["tflops"] = round(w["flops"] / (ms * 1e-3) / 1e12, 3)
+    out["kv_gbs"] = round(w["kv_bytes"] / (ms * 1e-3) / 1e9, 2)
+    out["bytes_gbs"] = round(w["bytes"] / (ms * 1e-3) / 1e9, 2)
+    if bound == "mfma":
+        out["frac_peak"] = round(out["tflops"] / PEAK_TFLOPS, 4)
+        if kms:
+            out["kernel_tflops"] = round(w["flops"] / (kms * 1e-3) / 1e12, 3)
+    else:
+        out["frac_peak"] = round(out["kv_gbs"] / PEAK_GBS, 4)
+        if kms:
+            out["kernel_kv_gbs"] = round(w["kv_bytes"] / (kms * 1e-3) / 1e9, 2)
+    return out
+
+
+def cpu_baseline(case, w):
+    """Strict ggml-CPU-semantics oracle on the full workload, this host."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle
+
+    n_threads = max(1, min(16, (os.cpu_count() or 2) // 2))   # reference: hardware_concurrency()/2
+    oracle.fa_ggml(case.q, case.k, case.v, case.mask, case.scale, n_threads=n_threads)   # warm-up
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle.fa_ggml(case.q, case.k, case.v, case.mask, case.scale, n_threads=n_threads)
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    cpu = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return dict(value=round(w["flops"] / t / 1e12, 5), unit="TFLOP/s", cores=n_threads, kind="port",
+                sample=f"full C2 workload (2048 q x 32 heads, causal), median of 3 runs, {t:.3f} s each; "
+                       f"ggml-CPU-semantics oracle (fp16 V accumulator, AVX2); host CPU: {cpu}")
+
+
+def traffic_from_profiles():
+    p = os.path.join(REPO, "profiles", "fa_prefill_c2_traffic.json")
+    if not os.path.exists(p):
+        return None
+    try:
+        with open(p) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this engine is measured on one GPU; --gpus {args.gpus} is not supported "
+              f"(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import mxfa
+    from mxfa import cases as C
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    names = [n.strip() for n in args.only.split(",") if n.strip()]
+    if "c2" not in names:
+        names.insert(0, "c2")
+    results = {}
+    headline = None
+    for name in names:
+        log(f"[bench] building {name} ...")
+        case = C.BUILDERS[name]()
+        # supports_op reads descriptors only: a placeholder aligned address will do
+        fake = lambda t: mxfa.DeviceView(t.type, tuple(t.ne), tuple(t.nb), 1 << 20)  # noqa: E731
+        ok = mxfa.supports(fake(case.q), fake(case.k), fake(case.v),
+                           fake(case.mask) if case.mask is not None else None, case.scale)
+        if not ok:
+            results[name] = dict(workload=DESCR[name], skipped=mxfa.last_error())
+            log(f"[bench] {name}: skipped ({mxfa.last_error()})")
+            continue
+        rot = ROTATE_BYTES if BOUND[name] == "hbm" else None
+        ms, kern, w, ncp = time_case(mxfa, torch, case, args.steps, args.warmup, rot)
+        results[name] = summarize(name, ms, kern, w, ncp)
+        log(f"[bench] {name}: {json.dumps(results[name])}")
+        if name == "c2":
+            headline = (case, w, ms, kern)
+
+    case, w, ms, kern = headline
+    kms = kern["fa_prefill"]
+    achieved = w["flops"] / (kms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": round(w["flops"] / (ms * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: Philox4x32-10 + Box-Muller N(0,1), seed 1002 (q stream 0, k 1, v 2)",
+        "config": {"workload": DESCR["c2"], "batch": 1, "seq_len": 2048, "n_heads": 32, "n_kv_heads": 8,
+                   "head_dim": 128, "q_type": "f32", "kv_type": "f16", "mask": "f16 causal",
+                   "accumulate": "fp32", "algorithmic_gflop": round(w["flops"] / 1e9, 3)},
+        "roofline": {"bound": "mfma", "kernel": "fa_prefill_kernel<F16>", "achieved": round(achieved, 3),
+                     "peak": PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_TFLOPS, 4),
+                     "kernel_ms": round(kms, 5), "traffic": traffic_from_profiles()},
+        "configs": results,
+    }
+    if not args.no_cpu:
+        log("[bench] timing the CPU baseline ...")
+        line["cpu_baseline"] = cpu_baseline(case, w)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -110,6 +110,17 @@ const char *mxfa_last_error(void);
 /* Library version: major*10000 + minor*100 + patch. */
 int mxfa_version(void);
 
+/* Per-kernel timing (a profiling aid; no counterpart in ggml).  While
+ * enabled, every kernel the engine launches is bracketed by two HIP events
+ * recorded on its launch stream.  mxfa_timing_read() waits for the recorded
+ * events, returns the summed duration (ms) and launch count of one kernel
+ * family ("fa_prefill", "mask_classify", "fa_split", "fa_combine") since the
+ * last reset, and mxfa_timing_reset() clears all counters.  Disabled by
+ * default; enabling it adds two event records per launch. */
+void mxfa_timing_enable(int on);
+int  mxfa_timing_read(const char *kernel, double *total_ms, int64_t *launches);
+void mxfa_timing_reset(void);
+
 #ifdef __cplusplus
 }
 #endif
