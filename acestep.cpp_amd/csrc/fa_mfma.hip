@@ -44,29 +44,60 @@ constexpr int kStageBytes = 2 * kTileBytes;  // K + V^T
 constexpr int kPfLds = 2 * kStageBytes;      // double buffered: 64 KB
 
 __global__ void __launch_bounds__(256) mask_classify_kernel(const FaArgs a, uint8_t *cls) {
+    // One workgroup per (key tile, query tile, mask plane).  Each row of the
+    // tile (64 keys = 128 B) is read by 16 lanes with 8-byte loads; the
+    // prefill path guarantees 8-byte aligned mask rows.
     const int kt = blockIdx.x, qt = blockIdx.y, plane = blockIdx.z;
     const int m2i = plane % a.m_ne2, m3i = plane / a.m_ne2;
     const char *base = a.mask + (int64_t)m2i * a.m_nb2 + (int64_t)m3i * a.m_nb3;
     const int q_lo = qt * kPfBM, k_lo = kt * kPfBN;
+    const int c4 = threadIdx.x & 15;           // 4-key group within the row
+    const int r0 = threadIdx.x >> 4;           // 16 rows per pass
+    const int k = k_lo + 4 * c4;
     int all_ninf = 1, all_zero = 1;
-    for (int i = threadIdx.x; i < kPfBM * kPfBN; i += 256) {
-        const int q = q_lo + (i >> 6), k = k_lo + (i & 63);
-        if (q < a.Sq && k < a.Skv) {
-            const uint16_t v = *(const uint16_t *)(base + (int64_t)q * a.m_nb1 + 2 * (int64_t)k);
-            all_ninf &= (v == 0xFC00u);
-            all_zero &= ((v & 0x7FFFu) == 0);
+#pragma unroll
+    for (int pass = 0; pass < kPfBM / 16; pass++) {
+        const int q = q_lo + r0 + 16 * pass;
+        if (q >= a.Sq || k >= a.Skv) continue;
+        const uint16_t *row = (const uint16_t *)(base + (int64_t)q * a.m_nb1);
+        if (k + 3 < a.Skv) {
+            const u16x4 v = *(const u16x4 *)(row + k);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                all_ninf &= (v[i] == 0xFC00u);
+                all_zero &= ((v[i] & 0x7FFFu) == 0);
+            }
+        } else {
+            for (int i = 0; i < 4 && k + i < a.Skv; i++) {
+                const uint16_t v = row[k + i];
+                all_ninf &= (v == 0xFC00u);
+                all_zero &= ((v & 0x7FFFu) == 0);
+            }
         }
     }
     all_ninf = __syncthreads_and(all_ninf);
     all_zero = __syncthreads_and(all_zero);
-    if (threadIdx.x == 0) cls[((int64_t)plane * a.n_qt + qt) * a.n_kt + kt] = all_ninf ? 0 : (all_zero ? 1 : 2);
+    if (threadIdx.x == 0) cls[((int64_t)plane * a.n_qt + qt) * a.n_kt_pad + kt] = all_ninf ? 0 : (all_zero ? 1 : 2);
 }
 
-__device__ __forceinline__ int next_live(const uint8_t *cls, int kt, int n) {
-    if (!cls) return kt;
-    while (kt < n && cls[kt] == 0) kt++;
-    return kt;
-}
+// Tile classes of one (plane, query tile) row live in registers: lane l
+// holds the class bytes of key tiles 4l..4l+3 (w0: tiles < 256, w1: tiles
+// 256..511), read with v_readlane (uniform, no memory wait in the loop).
+struct TileClasses {
+    uint32_t w0, w1;
+    bool present;
+    __device__ __forceinline__ int at(int kt) const {
+        if (!present) return 1;
+        const uint32_t w = kt < 256 ? __builtin_amdgcn_readlane(w0, (kt >> 2) & 63)
+                                    : __builtin_amdgcn_readlane(w1, ((kt - 256) >> 2) & 63);
+        return (int)((w >> (8 * (kt & 3))) & 0xFFu);
+    }
+    __device__ __forceinline__ int next_live(int kt, int n) const {
+        if (!present) return kt;
+        while (kt < n && at(kt) == 0) kt++;
+        return kt;
+    }
+};
 
 template <int T>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -103,7 +134,13 @@ fa_prefill_kernel(const FaArgs a) {
     }
 
     const int plane = a.mask ? (b % a.m_ne3) * a.m_ne2 + head % a.m_ne2 : 0;
-    const uint8_t *cls = a.tile_class ? a.tile_class + ((int64_t)plane * a.n_qt + qt) * a.n_kt : nullptr;
+    TileClasses tc{0u, 0u, a.tile_class != nullptr};
+    if (tc.present) {
+        const uint32_t *row = (const uint32_t *)(a.tile_class + ((int64_t)plane * a.n_qt + qt) * a.n_kt_pad);
+        const int lane4 = 4 * (tid & 63);
+        if (lane4 < a.n_kt) tc.w0 = row[lane4 >> 2];
+        if (256 + lane4 < a.n_kt) tc.w1 = row[(256 + lane4) >> 2];
+    }
     const uint16_t *mrow =
         a.mask ? (const uint16_t *)(a.mask + (int64_t)qrow_c * a.m_nb1 + (int64_t)(head % a.m_ne2) * a.m_nb2 +
                                     (int64_t)(b % a.m_ne3) * a.m_nb3)
@@ -116,9 +153,6 @@ fa_prefill_kernel(const FaArgs a) {
     const char *kbase = a.k + (int64_t)kvh * a.k_nb2 + (int64_t)bk * a.k_nb3;
     const char *vbase = a.v + (int64_t)kvh * a.v_nb2 + (int64_t)bk * a.v_nb3;
 
-    // staging assignment: 16-byte chunk dc of keys kq+16j (K) / 4kq+kk (V)
-    const int dc = tid & 15, kq = tid >> 4;
-
     f32x16 o[4];
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
@@ -126,77 +160,73 @@ fa_prefill_kernel(const FaArgs a) {
         for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
     float m2 = -INFINITY, lsum = 0.0f;
 
-    u16x8 kreg[4], vreg[4];
-    auto gload = [&](int kt) {
+    // Tile staging: each wave DMAs 16 keys of K and of V (4 instructions of
+    // 4 keys x 16 chunks); lane -> (key 4j + lane/16, slot lane%16), and the
+    // slot holds the swizzled logical chunk.  Keys past Skv re-read row
+    // Skv-1 (in bounds; their scores are forced to -inf).
+    const int dma_key = lane >> 4, dma_slot = lane & 15;
+    auto issue = [&](int kt, int stage) {
+        uint8_t *ks = smem + stage * kStageBytes;
+        uint8_t *vs = ks + kTileBytes;
         const int key0 = kt * kPfBN;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int key = min(key0 + kq + 16 * j, a.Skv - 1);
-            kreg[j] = *(const u16x8 *)(kbase + (int64_t)key * a.k_nb1 + 16 * dc);
-        }
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            const int key = min(key0 + 4 * kq + kk, a.Skv - 1);
-            vreg[kk] = *(const u16x8 *)(vbase + (int64_t)key * a.v_nb1 + 16 * dc);
+            const int krow = 16 * wave + 4 * j + dma_key;
+            const int key = min(key0 + krow, a.Skv - 1);
+            dma16(kbase + (int64_t)key * a.k_nb1 + 16 * (dma_slot ^ swz_k(krow)), ks + (16 * wave + 4 * j) * 256);
+            dma16(vbase + (int64_t)key * a.v_nb1 + 16 * (dma_slot ^ swz_v(krow)), vs + (16 * wave + 4 * j) * 256);
         }
     };
-    auto lstore = [&](int stage) {
-        uint8_t *ks = smem + stage * kStageBytes;
-        uint8_t *vs = ks + kTileBytes;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int key = kq + 16 * j;
-            *(u16x8 *)(ks + key * 256 + 16 * (dc ^ (key & 15))) = kreg[j];
-        }
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int d = 8 * dc + e;
-            const int slot = kq ^ ((d & 15) ^ ((d >> 4) & 7));
-            u16x4 w = {vreg[0][e], vreg[1][e], vreg[2][e], vreg[3][e]};
-            *(u16x4 *)(vs + d * 128 + 8 * slot) = w;
-        }
-    };
+
+    // transpose-read geometry of the V^T operand (see lds_read_tr16)
+    const int trg = lane >> 4, tri = lane & 15;
+    const int tr_h = trg >> 1, tr_ds = trg & 1;
 
     const int n_kt = a.n_kt;
-    int kt = next_live(cls, 0, n_kt);
-    if (kt < n_kt) {
-        gload(kt);
-        lstore(0);
-    }
-    __syncthreads();
+    int kt = tc.next_live(0, n_kt);
+    if (kt < n_kt) issue(kt, 0);
     int stage = 0;
     while (kt < n_kt) {
-        const int kn = next_live(cls, kt + 1, n_kt);
-        if (kn < n_kt) gload(kn);
-        const int cl = cls ? cls[kt] : 1;
+        const int kn = tc.next_live(kt + 1, n_kt);
+        if (kn < n_kt) {
+            issue(kn, stage ^ 1);
+            MXFA_WAIT_VMCNT(8);      // this tile's 8 copies done, next tile's in flight
+        } else {
+            MXFA_WAIT_VMCNT(0);
+        }
+        __builtin_amdgcn_s_barrier();
+        const int cl = tc.at(kt);
         const uint8_t *ks = smem + stage * kStageBytes;
         const uint8_t *vs = ks + kTileBytes;
-
-        // One 32-key half-tile: S^T = K . Q^T, online softmax, O^T += V^T . P^T.
-        // Interior unmasked tiles only scale the scores; tiles with mask
-        // entries, the Skv tail or a softcap take the general transform.
         const int key0 = kt * kPfBN;
         const bool tail = key0 + kPfBN > a.Skv;
         const bool general = cl == 2 || tail || use_softcap;
-#pragma unroll 1
-        for (int kb = 0; kb < 2; kb++) {
-            // lane: query l32, keys 32kb + 8(r/4) + 4h + r%4
-            f32x16 s;
+
+        // S^T = K . Q^T for the two 32-key halves (independent MFMA chains).
+        // lane: query l32, keys 32kb + 8(r/4) + 4h + r%4
+        f32x16 s[2];
 #pragma unroll
-            for (int r = 0; r < 16; r++) s[r] = 0.0f;
-            {
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) s[kb][r] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++) {
                 const int key = 32 * kb + l32;
-#pragma unroll
-                for (int t = 0; t < 8; t++) {
-                    const u16x8 av = *(const u16x8 *)(ks + key * 256 + 16 * ((2 * t + h) ^ (key & 15)));
-                    s = MF::run(__builtin_bit_cast(V8, av), qb[t], s);
-                }
+                const u16x8 av = *(const u16x8 *)(ks + key * 256 + 16 * ((2 * t + h) ^ swz_k(key)));
+                s[kb] = MF::run(__builtin_bit_cast(V8, av), qb[t], s[kb]);
             }
-            // scores -> exp2 domain
-            if (!general) {
+        }
+        // scores -> exp2 domain
+        if (!general) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) s[r] *= sl2;
-            } else {
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) s[kb][r] *= sl2;
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const int kbase4 = key0 + 32 * kb + 8 * j + 4 * h;
@@ -216,62 +246,71 @@ fa_prefill_kernel(const FaArgs a) {
                     for (int i = 0; i < 4; i++) {
                         const int r = 4 * j + i;
                         float xv;
-                        if (use_softcap) xv = (a.softcap * tanhf(s[r] * sc_in)) * kLog2e + mv[i];
-                        else xv = fmaf(s[r], sl2, mv[i]);
+                        if (use_softcap) xv = (a.softcap * tanhf(s[kb][r] * sc_in)) * kLog2e + mv[i];
+                        else xv = fmaf(s[kb][r], sl2, mv[i]);
                         if (mv[i] == -INFINITY || kbase4 + i >= a.Skv) xv = -INFINITY;
-                        s[r] = xv;
+                        s[kb][r] = xv;
                     }
                 }
+        }
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) bmax = fmaxf(bmax, s[kb][r]);
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        // Lazy rescale: the reference max m2 is raised only when some row's
+        // new max exceeds it by more than 8 (exp2 domain), so p <= 2^8 and
+        // O, l are rescaled on few tiles.  O and l always share the same
+        // reference, so the softmax is unchanged.
+        if (__any(bmax > m2 + 8.0f)) {
+            const float mnew = fmaxf(m2, bmax);
+            const float alpha = (mnew == -INFINITY) ? 1.0f : fast_exp2(m2 - mnew);
+            m2 = mnew;
+            lsum *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
+        }
+        const float m_use = (m2 == -INFINITY) ? 0.0f : m2;
+        // P^T operands of the four 16-key steps ks:
+        // k-slot 4u+i <-> key 16ks + 8u + 4h + i = register 8(ks&1) + 4u + i of s[ks>>1].
+        // The row sum adds exactly the rounded values the MFMA consumes.
+        V8 pb[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int kb = ks >> 1, rb = 8 * (ks & 1);
+            f32x4 lo, hi;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                lo[i] = fast_exp2(s[kb][rb + i] - m_use);       // exp2(-inf) = 0
+                hi[i] = fast_exp2(s[kb][rb + 4 + i] - m_use);
             }
-            float bmax = -INFINITY;
+            const u16x8 bits = cvt8<T>(lo, hi);
+            lsum = sum8<T>(bits, lsum);
+            pb[ks] = __builtin_bit_cast(V8, bits);
+        }
+        // O^T += V^T . P^T; the V^T operand comes from two transpose reads of
+        // the row-major V tile (keys 16ks + 8u + 4h + e, dims 32dt + l32).
 #pragma unroll
-            for (int r = 0; r < 16; r++) bmax = fmaxf(bmax, s[r]);
-            bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-            // Lazy rescale: the reference max m2 is raised only when some
-            // row's new max exceeds it by more than 8 (exp2 domain), so
-            // p <= 2^8 and O, l are rescaled on few tiles.  O and l always
-            // share the same reference, so the softmax is unchanged.
-            if (__any(bmax > m2 + 8.0f)) {
-                const float mnew = fmaxf(m2, bmax);
-                const float alpha = (mnew == -INFINITY) ? 1.0f : fast_exp2(m2 - mnew);
-                m2 = mnew;
-                lsum *= alpha;
+        for (int dt = 0; dt < 4; dt++) {
 #pragma unroll
-                for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
-            }
-            const float m_use = (m2 == -INFINITY) ? 0.0f : m2;
+            for (int ks = 0; ks < 4; ks++) {
+                u16x4 part[2];
 #pragma unroll
-            for (int r = 0; r < 16; r++) s[r] = fast_exp2(s[r] - m_use);   // exp2(-inf) = 0
-            // P^T operands of the two 16-key steps ks = 2kb + u2:
-            // k-slot 4u+i <-> key 16ks + 8u + 4h + i = register 8u2 + 4u + i.
-            // The row sum adds the same rounded values the MFMA consumes.
-            V8 pb[2];
-#pragma unroll
-            for (int u2 = 0; u2 < 2; u2++) {
-                const int rb = 8 * u2;
-                const u16x8 bits = cvt8<T>(f32x4{s[rb + 0], s[rb + 1], s[rb + 2], s[rb + 3]},
-                                           f32x4{s[rb + 4], s[rb + 5], s[rb + 6], s[rb + 7]});
-                lsum = sum8<T>(bits, lsum);
-                pb[u2] = __builtin_bit_cast(V8, bits);
-            }
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++) {
-                const int d = 32 * dt + l32;
-                const int sw = (d & 15) ^ ((d >> 4) & 7);
-                const uint8_t *vrow = vs + d * 128;
-#pragma unroll
-                for (int u2 = 0; u2 < 2; u2++) {
-                    const int ksi = 2 * kb + u2;
-                    const u16x4 lo = *(const u16x4 *)(vrow + 8 * ((4 * ksi + h) ^ sw));
-                    const u16x4 hi = *(const u16x4 *)(vrow + 8 * ((4 * ksi + 2 + h) ^ sw));
-                    const u16x8 av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    o[dt] = MF::run(__builtin_bit_cast(V8, av), pb[u2], o[dt]);
+                for (int u = 0; u < 2; u++) {
+                    const int key = 16 * ks + 8 * u + 4 * tr_h + (tri >> 2);
+                    const int c = 4 * dt + 2 * tr_ds + ((tri & 3) >> 1);
+                    part[u] = lds_read_tr16(vs + key * 256 + 16 * (c ^ swz_v(key)) + 8 * (tri & 1));
                 }
+                const u16x8 av = {part[0][0], part[0][1], part[0][2], part[0][3],
+                                  part[1][0], part[1][1], part[1][2], part[1][3]};
+                o[dt] = MF::run(__builtin_bit_cast(V8, av), pb[ks], o[dt]);
             }
         }
-
-        if (kn < n_kt) lstore(stage ^ 1);
-        __syncthreads();
+        // every LDS read of this stage has returned before anyone refills it
+        MXFA_WAIT_LGKMCNT0();
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
         stage ^= 1;
         kt = kn;
     }

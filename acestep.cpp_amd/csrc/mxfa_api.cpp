@@ -181,12 +181,15 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
 
     const bool mask_vec_ok = !mask || (is_aligned(mask->data, 8) && mask->nb[1] % 8 == 0 && mask->nb[2] % 8 == 0 &&
                                        mask->nb[3] % 8 == 0);
-    pl.prefill = (k->type == MXFA_TYPE_F16 || k->type == MXFA_TYPE_BF16) && a.Sq >= kPrefillMinSq && mask_vec_ok;
+    const int64_t n_kt = (a.Skv + kPfBN - 1) / kPfBN;
+    pl.prefill = (k->type == MXFA_TYPE_F16 || k->type == MXFA_TYPE_BF16) && a.Sq >= kPrefillMinSq && mask_vec_ok &&
+                 (!mask || n_kt <= kPfMaxKeyTiles);
     if (pl.prefill) {
         a.n_qt = (a.Sq + kPfBM - 1) / kPfBM;
-        a.n_kt = (a.Skv + kPfBN - 1) / kPfBN;
+        a.n_kt = (int32_t)n_kt;
+        a.n_kt_pad = (a.n_kt + 3) & ~3;
         pl.n_planes = mask ? a.m_ne2 * a.m_ne3 : 0;
-        pl.ws_bytes = mask ? (size_t)pl.n_planes * a.n_qt * a.n_kt : 0;
+        pl.ws_bytes = mask ? (size_t)pl.n_planes * a.n_qt * a.n_kt_pad : 0;
         a.n_splits = 1;
         a.chunk = a.Skv;
         return;

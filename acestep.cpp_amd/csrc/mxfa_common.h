@@ -50,6 +50,7 @@ struct FaArgs {
     // prefill: per (mask plane, q tile, k tile) class (see fa_mfma.hip)
     const uint8_t *tile_class;
     int32_t n_qt, n_kt;                   // tiles along Sq and Skv
+    int32_t n_kt_pad;                     // class row stride (n_kt rounded up to 4)
 };
 
 // MFMA 16x16x32 for the two 16-bit float formats (8 k-values per lane).
@@ -143,5 +144,35 @@ __device__ __forceinline__ float alibi_slope(const FaArgs &a, int h) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
+// lgkmcnt[11:8] | vmcnt[5:4] << 14).
+#define MXFA_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+#define MXFA_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(0xC07F)
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Direct HBM -> LDS copy of 16 bytes per lane: lane l's bytes land at
+// lds_base + 16*l (lds_base must be the same for the whole wave).
+__device__ __forceinline__ void dma16(const void *g, void *lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void *)lds_base, 16, 0, 0);
+}
+
+// LDS transpose read of four 16-bit values.  Within each group of 16 lanes,
+// lane j receives element (j % 4) of the 8-byte chunks addressed by lanes
+// j/4 + 4e, e = 0..3 (gfx950 ds_read_b64_tr_b16).
+__device__ __forceinline__ u16x4 lds_read_tr16(const void *p) {
+    return __builtin_bit_cast(u16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)p));
+}
+
+// XOR swizzles of the 16-byte chunks of a 256-byte K or V row stored in
+// LDS (key k, logical chunk c at slot c ^ swz(k)).  K: consecutive keys
+// read the same chunk (MFMA A operand), k & 15 spreads them over all banks.
+// V: transpose reads fetch 4 consecutive keys x 32 bytes per 16 lanes;
+// swz_v keeps those (and the neighbouring 16-lane group) conflict-free.
+__device__ __forceinline__ int swz_k(int k) { return k & 15; }
+__device__ __forceinline__ int swz_v(int k) { return (((k & 3) << 1) ^ ((k & 1) << 3)) ^ (((k >> 2) & 1) << 1); }
 
 }  // namespace mxfa

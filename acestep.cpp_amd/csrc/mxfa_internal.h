@@ -18,8 +18,10 @@ hipError_t launch_fa_split_q8(const FaArgs &a, hipStream_t stream);
 constexpr int kPfBM = 128;   // query rows per workgroup (4 waves x 32)
 constexpr int kPfBN = 64;    // keys per K/V tile
 
-// Mask tile classifier: writes a.tile_class[plane][qt][kt] for every
-// (mask plane, kPfBM-query tile, kPfBN-key tile).
+// Mask tile classifier: writes a.tile_class[plane][qt][kt] (row stride
+// a.n_kt_pad bytes) for every (mask plane, kPfBM-query tile, kPfBN-key
+// tile): 0 = all -inf, 1 = all zero, 2 = anything else.
+constexpr int kPfMaxKeyTiles = 512;   // class rows held in two registers per lane
 hipError_t launch_mask_classify(const FaArgs &a, int n_planes, uint8_t *classes, hipStream_t stream);
 
 // MFMA prefill / DiT kernel.  ktype: T_F16/T_BF16.
