@@ -156,8 +156,20 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 // Direct HBM -> LDS copy of 16 bytes per lane: lane l's bytes land at
 // lds_base + 16*l (lds_base must be the same for the whole wave).
+//
+// Issued as inline assembly on purpose: the compiler's own wait insertion
+// treats every LDS read after such a copy as a possible alias and drains
+// all outstanding copies (vmcnt(0)) before it, which serialises a
+// multi-buffer prefetch.  Callers wait with MXFA_WAIT_VMCNT before reading a
+// buffer.  Compiler-generated waits for other vector loads stay correct: a
+// copy unknown to the compiler only makes them wait longer (counters retire
+// in order).
 __device__ __forceinline__ void dma16(const void *g, void *lds_base) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void *)lds_base, 16, 0, 0);
+    const uint32_t lds_addr = (uint32_t)(uintptr_t)(lds_void *)lds_base;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(g)
+                 : "memory", "m0");
 }
 
 // LDS transpose read of four 16-bit values.  Within each group of 16 lanes,
