@@ -2,15 +2,18 @@
 //
 // Validates ggml-style descriptors (the same contract ggml_flash_attn_ext
 // asserts), picks a kernel and launches it on the caller's stream:
-//   * split-KV kernel (fa_split.hip) when few query rows share a KV head:
-//     decode (Sq = 1) and short prompts, and Q8_0 K/V;
+//   * split-KV decode kernel (fa_decode.hip) when few query rows share a
+//     KV head: decode (Sq = 1) and short prompts, and every Q8_0 K/V call;
 //   * MFMA prefill kernel (fa_mfma.hip) for long query runs (prefill, DiT),
 //     preceded by the mask tile classifier when a mask is given.
-// The only memory the engine owns is a per-device, grow-only workspace
-// (split partials, mask tile classes), freed by mxfa_release().
+// The only memory the engine owns is per device and grow-only: a workspace
+// (split partials, mask tile classes) and the split tickets, freed by
+// mxfa_release().  Calls that overlap on one device (different streams)
+// share them and must be serialised by the caller.
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdarg>
@@ -42,15 +45,18 @@ int fail(int code, const char *fmt, ...) {
 struct Workspace {
     void *ptr = nullptr;
     size_t size = 0;
+    int *tickets = nullptr;   // zero between calls
+    int64_t n_tickets = 0;
 };
 std::mutex g_ws_mu;
 std::vector<Workspace> g_ws;  // indexed by HIP device id
 
 // Query-run length from which the MFMA prefill kernel is used.
 constexpr int64_t kPrefillMinSq = 64;
-// Workgroups the split kernel aims for before it splits the KV range.
-constexpr int64_t kSplitTargetWgs = 1024;
+// Workgroups the decode kernel aims for before it splits the KV range.
+constexpr int64_t kSplitTargetWgs = 512;
 constexpr int kSplitKeyQuantum = 128;  // 4 waves x 32 keys
+constexpr int64_t kMaxDecodeSplits = 64;   // merge capacity of the decode kernel
 
 bool is_aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
@@ -80,6 +86,7 @@ struct Plan {
     int ktype = 0;
     int n_planes = 0;
     size_t ws_bytes = 0;
+    int64_t n_tickets = 0;
 };
 
 // Full validation.  Returns MXFA_OK, MXFA_ERR_INVALID (malformed) or
@@ -179,8 +186,15 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     a.m1 = std::pow(2.0f, -(p->max_bias / 2.0f) / (float)a.n_head_log2);
     pl.ktype = k->type;
 
-    const bool mask_vec_ok = !mask || (is_aligned(mask->data, 8) && mask->nb[1] % 8 == 0 && mask->nb[2] % 8 == 0 &&
-                                       mask->nb[3] % 8 == 0);
+    auto mask_rows_aligned = [&](size_t al) {
+        return mask && is_aligned(mask->data, al) && mask->nb[1] % al == 0 && mask->nb[2] % al == 0 &&
+               mask->nb[3] % al == 0;
+    };
+    a.mask_al8 = mask_rows_aligned(8);
+    a.mask_al16 = mask_rows_aligned(16);
+    a.mask_vec4 = a.mask_al8 && mask->ne[0] >= ((k->ne[1] + 3) & ~(int64_t)3);
+    a.mask_vec16 = a.mask_vec4 && mask->ne[0] >= 16;
+    const bool mask_vec_ok = !mask || a.mask_al8;
     const int64_t n_kt = (a.Skv + kPfBN - 1) / kPfBN;
     pl.prefill = (k->type == MXFA_TYPE_F16 || k->type == MXFA_TYPE_BF16) && a.Sq >= kPrefillMinSq && mask_vec_ok &&
                  (!mask || n_kt <= kPfMaxKeyTiles);
@@ -198,7 +212,8 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     const int64_t base = (int64_t)a.B * a.Nkv * a.row_tiles;
     const int64_t max_splits = (a.Skv + kSplitKeyQuantum - 1) / kSplitKeyQuantum;
     int64_t n_splits = 1;
-    if (base < kSplitTargetWgs) n_splits = std::min<int64_t>(max_splits, (kSplitTargetWgs + base - 1) / base);
+    if (base < kSplitTargetWgs)
+        n_splits = std::min<int64_t>({max_splits, (kSplitTargetWgs + base - 1) / base, kMaxDecodeSplits});
     int64_t chunk = (a.Skv + n_splits - 1) / n_splits;
     chunk = (chunk + kSplitKeyQuantum - 1) / kSplitKeyQuantum * kSplitKeyQuantum;
     n_splits = (a.Skv + chunk - 1) / chunk;
@@ -207,12 +222,14 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     if (n_splits > 1) {
         const size_t rows = (size_t)a.B * a.Nkv * a.M * n_splits;
         pl.ws_bytes = rows * kD * sizeof(float) + rows * 2 * sizeof(float);
+        pl.n_tickets = (int64_t)a.B * a.Nkv * a.row_tiles;
     }
 }
 
-int ensure_workspace(size_t bytes, hipStream_t stream, void **out) {
+int ensure_workspace(size_t bytes, int64_t n_tickets, hipStream_t stream, void **out, int **tickets) {
     *out = nullptr;
-    if (bytes == 0) return MXFA_OK;
+    *tickets = nullptr;
+    if (bytes == 0 && n_tickets == 0) return MXFA_OK;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return fail(MXFA_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
@@ -237,7 +254,30 @@ int ensure_workspace(size_t bytes, hipStream_t stream, void **out) {
         }
         ws.size = want;
     }
+    if (ws.n_tickets < n_tickets) {
+        if (ws.tickets) {
+            e = hipStreamSynchronize(stream);
+            if (e != hipSuccess) return fail(MXFA_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+            (void)hipFree(ws.tickets);
+            ws.tickets = nullptr;
+            ws.n_tickets = 0;
+        }
+        const int64_t want = std::max<int64_t>(1024, n_tickets + n_tickets / 4);
+        e = hipMalloc((void **)&ws.tickets, (size_t)want * sizeof(int));
+        if (e != hipSuccess) {
+            ws.tickets = nullptr;
+            return fail(MXFA_ERR_NOMEM, "hipMalloc(tickets): %s", hipGetErrorString(e));
+        }
+        e = launch_fill_zero(ws.tickets, want, stream);
+        if (e != hipSuccess) {
+            (void)hipFree(ws.tickets);
+            ws.tickets = nullptr;
+            return fail(MXFA_ERR_HIP, "ticket fill: %s", hipGetErrorString(e));
+        }
+        ws.n_tickets = want;
+    }
     *out = ws.ptr;
+    *tickets = ws.tickets;
     return MXFA_OK;
 }
 
@@ -316,14 +356,10 @@ int mxfa_supports(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor 
                   const mxfa_params *params, const mxfa_tensor *dst) {
     const int rc = check(q, k, v, mask, params, dst);
     if (rc != MXFA_OK) return 0;
-    if (k->type == MXFA_TYPE_Q8_0) {
-        fail(MXFA_ERR_UNSUPPORTED, "Q8_0 K/V not built in this library");
-        return 0;
-    }
     Plan pl;
     make_plan(q, k, v, mask, params, nullptr, pl);
     if (!pl.prefill && (int64_t)pl.args.Nkv * pl.args.row_tiles > 65535) {
-        fail(MXFA_ERR_UNSUPPORTED, "too many query rows per KV head for the split kernel");
+        fail(MXFA_ERR_UNSUPPORTED, "too many query rows per KV head for the decode kernel");
         return 0;
     }
     return 1;
@@ -334,14 +370,14 @@ int mxfa_flash_attn_ext(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_t
     if (!dst) return fail(MXFA_ERR_INVALID, "dst is required");
     int rc = check(q, k, v, mask, params, dst);
     if (rc != MXFA_OK) return rc;
-    if (k->type == MXFA_TYPE_Q8_0) return fail(MXFA_ERR_UNSUPPORTED, "Q8_0 K/V not built in this library");
     hipStream_t stream = (hipStream_t)hip_stream;
     Plan pl;
     make_plan(q, k, v, mask, params, dst, pl);
     void *ws = nullptr;
     if (!pl.prefill && (int64_t)pl.args.Nkv * pl.args.row_tiles > 65535)
-        return fail(MXFA_ERR_UNSUPPORTED, "too many query rows per KV head for the split kernel");
-    rc = ensure_workspace(pl.ws_bytes, stream, &ws);
+        return fail(MXFA_ERR_UNSUPPORTED, "too many query rows per KV head for the decode kernel");
+    int *tickets = nullptr;
+    rc = ensure_workspace(pl.ws_bytes, pl.n_tickets, stream, &ws, &tickets);
     if (rc != MXFA_OK) return rc;
     FaArgs &a = pl.args;
     hipError_t e;
@@ -361,9 +397,10 @@ int mxfa_flash_attn_ext(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_t
         const size_t rows = (size_t)a.B * a.Nkv * a.M * a.n_splits;
         a.part_o = (float *)ws;
         a.part_ml = a.part_o + rows * kD;
+        a.tickets = tickets;
     }
-    e = launch_fa_split(a, pl.ktype, stream);
-    if (e != hipSuccess) return fail(MXFA_ERR_HIP, "split launch: %s", hipGetErrorString(e));
+    e = launch_fa_decode(a, pl.ktype, stream);
+    if (e != hipSuccess) return fail(MXFA_ERR_HIP, "decode launch: %s", hipGetErrorString(e));
     return MXFA_OK;
 }
 
@@ -372,10 +409,11 @@ void mxfa_release(void) {
     int cur = 0;
     const bool have_cur = hipGetDevice(&cur) == hipSuccess;
     for (size_t d = 0; d < g_ws.size(); d++) {
-        if (!g_ws[d].ptr) continue;
+        if (!g_ws[d].ptr && !g_ws[d].tickets) continue;
         if (hipSetDevice((int)d) == hipSuccess) {
             (void)hipDeviceSynchronize();
-            (void)hipFree(g_ws[d].ptr);
+            if (g_ws[d].ptr) (void)hipFree(g_ws[d].ptr);
+            if (g_ws[d].tickets) (void)hipFree(g_ws[d].tickets);
         }
         g_ws[d] = Workspace{};
     }

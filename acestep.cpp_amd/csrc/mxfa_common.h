@@ -40,13 +40,18 @@ struct FaArgs {
     int32_t m_ne2, m_ne3;
     int32_t Sq, Nh, B, Skv, Nkv, G, rk3;  // G = Nh/Nkv, rk3 = B/Bk
     int32_t M;                            // rows per (b, kv head) = Sq*G
-    int32_t row_tiles;                    // split kernel: ceil(M/16)
+    int32_t row_tiles;                    // decode kernel: ceil(M/16)
     float scale, softcap;                 // softcap == 0: off
     float max_bias, m0, m1;               // ALiBi (max_bias == 0: off)
     uint32_t n_head_log2;
+    // mask row alignment (8 / 16 bytes for every row start); mask_vec4:
+    // 8-byte aligned rows holding at least round_up(Skv, 4) entries;
+    // mask_vec16: the same with at least 16 entries (16-key DMA blocks)
+    int32_t mask_al8, mask_al16, mask_vec4, mask_vec16;
     // split-KV
     int32_t n_splits, chunk;
     float *part_o, *part_ml;
+    int *tickets;                         // one per (b, kv head, row tile), zero between calls
     // prefill: per (mask plane, q tile, k tile) class (see fa_mfma.hip)
     const uint8_t *tile_class;
     int32_t n_qt, n_kt;                   // tiles along Sq and Skv
@@ -167,6 +172,16 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 __device__ __forceinline__ void dma16(const void *g, void *lds_base) {
     const uint32_t lds_addr = (uint32_t)(uintptr_t)(lds_void *)lds_base;
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(g)
+                 : "memory", "m0");
+}
+
+// Direct HBM -> LDS copy of 4 bytes per lane (4-byte aligned source): lane
+// l's bytes land at lds_base + 4*l.  Same contract as dma16.
+__device__ __forceinline__ void dma4(const void *g, void *lds_base) {
+    const uint32_t lds_addr = (uint32_t)(uintptr_t)(lds_void *)lds_base;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
                  :
                  : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(g)
                  : "memory", "m0");

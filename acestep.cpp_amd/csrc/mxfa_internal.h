@@ -8,11 +8,13 @@
 
 namespace mxfa {
 
-// Split-KV kernel (+ combine pass when a.n_splits > 1).  ktype: T_F16/T_BF16.
-hipError_t launch_fa_split(const FaArgs &a, int ktype, hipStream_t stream);
+// Split-KV decode kernel, F16/BF16/Q8_0 K/V.  With a.n_splits > 1 it needs
+// a.part_o / a.part_ml and a.tickets (B*Nkv*row_tiles ints, zero on entry;
+// left zero on exit).
+hipError_t launch_fa_decode(const FaArgs &a, int ktype, hipStream_t stream);
 
-// Split-KV kernel over Q8_0 K/V (+ combine pass when a.n_splits > 1).
-hipError_t launch_fa_split_q8(const FaArgs &a, hipStream_t stream);
+// Zero-fills n ints (ticket buffer set-up).
+hipError_t launch_fill_zero(int *p, int64_t n, hipStream_t stream);
 
 // MFMA prefill kernel geometry.
 constexpr int kPfBM = 128;   // query rows per workgroup (4 waves x 32)

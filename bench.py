@@ -52,8 +52,8 @@ DESCR = {
     "c5": "Qwen3-4B decode over Q8_0 KV: B=4, 32/8 heads, D=128, KV 8192",
 }
 BOUND = {"c1": "hbm", "c2": "mfma", "c3": "hbm", "c4s": "mfma", "c4x": "hbm", "c5": "hbm"}
-KERNEL = {"c1": "fa_split", "c2": "fa_prefill", "c3": "fa_split", "c4s": "fa_prefill", "c4x": "fa_prefill",
-          "c5": "fa_split"}
+KERNEL = {"c1": "fa_decode", "c2": "fa_prefill", "c3": "fa_decode", "c4s": "fa_prefill", "c4x": "fa_prefill",
+          "c5": "fa_decode"}
 
 
 def log(*a):
@@ -108,7 +108,7 @@ def time_case(mx, torch, case, steps, warmup, rotate_bytes=None):
     torch.cuda.synchronize()
     mx.timing_enable(False)
     kern = {}
-    for fam in ("fa_prefill", "mask_classify", "fa_split", "fa_combine"):
+    for fam in ("fa_prefill", "mask_classify", "fa_decode"):
         tot, n = mx.timing_read(fam)
         if n:
             kern[fam] = tot / n

@@ -114,7 +114,7 @@ int mxfa_version(void);
  * enabled, every kernel the engine launches is bracketed by two HIP events
  * recorded on its launch stream.  mxfa_timing_read() waits for the recorded
  * events, returns the summed duration (ms) and launch count of one kernel
- * family ("fa_prefill", "mask_classify", "fa_split", "fa_combine") since the
+ * family ("fa_prefill", "mask_classify", "fa_decode") since the
  * last reset, and mxfa_timing_reset() clears all counters.  Disabled by
  * default; enabling it adds two event records per launch. */
 void mxfa_timing_enable(int on);

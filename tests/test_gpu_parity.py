@@ -170,10 +170,18 @@ def _rand_case(seed, B=2, Bk=None, Sq=5, Nh=8, Nkv=2, Skv=300, kv_type=1, mask="
         q = HostView(0, (D, Sq, Nh, B), (4, Nh * D * 4, D * 4, Nh * D * Sq * 4), mem.reshape(-1))
     else:
         q = HostView(0, (D, Sq, Nh, B), (4, D * 4, D * Sq * 4, D * Sq * Nh * 4), qa.reshape(-1))
-    conv = to_bf16_bits if kv_type == 30 else to_f16_bits
-    ka = conv(rng.standard_normal((Bk, Nkv, Skv, D)).astype(np.float32)).reshape(-1)
-    va = conv(rng.standard_normal((Bk, Nkv, Skv, D)).astype(np.float32)).reshape(-1)
-    nb = (2, 2 * D, 2 * D * Skv, 2 * D * Skv * Nkv)
+    if kv_type == 8:
+        from mxfa.cases import quantize_q8_0
+
+        ka = quantize_q8_0(rng.standard_normal((Bk, Nkv, Skv, D)).astype(np.float32).reshape(-1))
+        va = quantize_q8_0(rng.standard_normal((Bk, Nkv, Skv, D)).astype(np.float32).reshape(-1))
+        row = D // 32 * 34
+        nb = (34, row, row * Skv, row * Skv * Nkv)
+    else:
+        conv = to_bf16_bits if kv_type == 30 else to_f16_bits
+        ka = conv(rng.standard_normal((Bk, Nkv, Skv, D)).astype(np.float32)).reshape(-1)
+        va = conv(rng.standard_normal((Bk, Nkv, Skv, D)).astype(np.float32)).reshape(-1)
+        nb = (2, 2 * D, 2 * D * Skv, 2 * D * Skv * Nkv)
     k = HostView(kv_type, (D, Skv, Nkv, Bk), nb, ka)
     v = HostView(kv_type, (D, Skv, Nkv, Bk), nb, va)
     m = None
@@ -250,6 +258,42 @@ def test_bf16_kv(mx):
     for Sq in (1, 96):
         c = _rand_case(70 + Sq, B=2, Sq=Sq, Nh=8, Nkv=4, Skv=211, kv_type=30)
         check(mx, c, f"bf16 Sq={Sq}", bf16=True)
+
+
+@pytest.mark.parametrize("Sq,Skv,mask", [(1, 333, "random"), (3, 333, None), (1, 8, "random"),
+                                         (70, 190, "causal")])
+def test_q8_0_shapes(mx, Sq, Skv, mask):
+    # Q8_0 K/V always run the split-KV kernel (int8 MFMA on Q8_0-quantised Q)
+    c = _rand_case(90 + Sq + Skv, B=2, Sq=Sq, Nh=8, Nkv=2, Skv=Skv, kv_type=8, mask=mask)
+    check(mx, c, f"q8_0 Sq={Sq} Skv={Skv} mask={mask}")
+
+
+def test_q8_0_broadcast_softcap_alibi(mx):
+    c = _rand_case(95, B=4, Bk=1, Sq=2, Nh=8, Nkv=1, Skv=257, kv_type=8, mask_heads=8)
+    check(mx, c, "q8_0 bk broadcast + per-head mask")
+    c = _rand_case(96, B=1, Sq=4, Nh=16, Nkv=4, Skv=129, kv_type=8, softcap=30.0)
+    check(mx, c, "q8_0 softcap")
+    c = _rand_case(97, B=1, Sq=4, Nh=16, Nkv=4, Skv=129, kv_type=8, max_bias=8.0)
+    check(mx, c, "q8_0 alibi")
+
+
+def test_unaligned_and_short_masks(mx):
+    """Mask rows that are only 2-byte aligned (scalar mask reads) and masks
+    shorter than one 16-key DMA block take the register-streaming kernel."""
+    from mxfa.cases import HostView
+
+    c = _rand_case(110, B=2, Sq=2, Nh=8, Nkv=2, Skv=301)
+    Skv, Sq, Hm, B = c.mask.ne
+    pitch = Skv + 1                       # odd row pitch: rows 2-byte aligned
+    src = c.mask.buf.reshape(B, Hm, Sq, Skv)
+    buf = np.full(B * Hm * Sq * pitch + 1, 0xFC00, dtype=np.uint16)
+    dst = buf[1:].reshape(B, Hm, Sq, pitch)
+    dst[..., :Skv] = src
+    c.mask = HostView(1, (Skv, Sq, Hm, B), (2, 2 * pitch, 2 * pitch * Sq, 2 * pitch * Sq * Hm), buf, offset=2)
+    check(mx, c, "2-byte aligned mask rows")
+    for Skv in (5, 12):
+        c = _rand_case(120 + Skv, B=1, Sq=1, Nh=4, Nkv=2, Skv=Skv)
+        check(mx, c, f"short window Skv={Skv}")
 
 
 def test_causal_prefill_offsets(mx):
