@@ -42,6 +42,8 @@ METRIC = "FA TFLOP/s (prefill/DiT) + decode KV GB/s, % of MI355X roofline, 1 GPU
 PEAK_TFLOPS = 2500.0     # MI355X dense fp16/bf16 MFMA
 PEAK_GBS = 8000.0        # MI355X HBM3E
 ROTATE_BYTES = 600e6     # > 256 MB Infinity Cache
+COPY_BYTES = 1 << 30     # calibration copy: 1 GiB read + 1 GiB written
+CPU_SAMPLE_S = 12.0      # seconds of CPU work for the cpu_baseline sample
 
 DESCR = {
     "c1": "Qwen3-0.6B decode: B=1, 1 token, 16/8 heads, D=128, KV 512 (F16 cache view, zero mask)",
@@ -146,7 +148,8 @@ def cpu_baseline(case, w):
     n_threads = max(1, min(16, (os.cpu_count() or 2) // 2))   # reference: hardware_concurrency()/2
     oracle.fa_ggml(case.q, case.k, case.v, case.mask, case.scale, n_threads=n_threads)   # warm-up
     ts = []
-    for _ in range(3):
+    t_start = time.perf_counter()
+    while len(ts) < 3 or (time.perf_counter() - t_start < CPU_SAMPLE_S and len(ts) < 200):
         t0 = time.perf_counter()
         oracle.fa_ggml(case.q, case.k, case.v, case.mask, case.scale, n_threads=n_threads)
         ts.append(time.perf_counter() - t0)
@@ -161,19 +164,41 @@ def cpu_baseline(case, w):
     except OSError:
         pass
     return dict(value=round(w["flops"] / t / 1e12, 5), unit="TFLOP/s", cores=n_threads, kind="port",
-                sample=f"full C2 workload (2048 q x 32 heads, causal), median of 3 runs, {t:.3f} s each; "
-                       f"ggml-CPU-semantics oracle (fp16 V accumulator, AVX2); host CPU: {cpu}")
+                sample=f"full C2 workload (2048 q x 32 heads, causal) repeated for ~{CPU_SAMPLE_S:.0f} s: "
+                       f"median of {len(ts)} runs, {t:.3f} s each; ggml-CPU-semantics C oracle (fp16 V "
+                       f"accumulator, AVX2 reduction order), {n_threads} threads; host CPU: {cpu}")
+
+
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "fa_prefill_c2_traffic.md")
 
 
 def traffic_from_profiles():
-    p = os.path.join(REPO, "profiles", "fa_prefill_c2_traffic.json")
-    if not os.path.exists(p):
+    """HBM bytes per fa_prefill launch on C2, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (line `hbm_bytes_per_launch: N`)."""
+    if not os.path.exists(TRAFFIC_FILE):
         return None
     try:
-        with open(p) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.strip().startswith("hbm_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1].strip()))
     except (OSError, ValueError):
         return None
+    return None
+
+
+def calibrate_copy(steps):
+    """A plain device-to-device copy of COPY_BYTES, for scaling the
+    FETCH_SIZE / WRITE_SIZE counters (run under rocprofv3 --pmc)."""
+    import torch
+
+    n = COPY_BYTES // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": COPY_BYTES, "launches": steps}), flush=True)
 
 
 def main():
@@ -183,6 +208,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB copy (counter calibration under rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this engine is measured on one GPU; --gpus {args.gpus} is not supported "
@@ -191,10 +218,14 @@ def main():
 
     import torch
 
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.calibrate_copy:
+        calibrate_copy(args.steps)
+        return
+
     import mxfa
     from mxfa import cases as C
 
-    assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
     names = [n.strip() for n in args.only.split(",") if n.strip()]
     if "c2" not in names:
