@@ -149,7 +149,7 @@ def cpu_baseline(case, w):
     oracle.fa_ggml(case.q, case.k, case.v, case.mask, case.scale, n_threads=n_threads)   # warm-up
     ts = []
     t_start = time.perf_counter()
-    while len(ts) < 3 or (time.perf_counter() - t_start < CPU_SAMPLE_S and len(ts) < 200):
+    while len(ts) < 5 or (time.perf_counter() - t_start < CPU_SAMPLE_S and len(ts) < 200):
         t0 = time.perf_counter()
         oracle.fa_ggml(case.q, case.k, case.v, case.mask, case.scale, n_threads=n_threads)
         ts.append(time.perf_counter() - t0)

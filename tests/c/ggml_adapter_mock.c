@@ -1,0 +1,76 @@
+/* Compiles include/mxfa_ggml.h against a mock struct ggml_tensor (the
+ * fields the adapter reads, in ggml's order) and prints the descriptors it
+ * derives from a flash-attention node, plus mxfa_supports()'s verdict.
+ * Built and run by tests/test_ggml_adapter.py. */
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#define MOCK_MAX_SRC 10
+struct ggml_tensor {
+    int type;                                  /* enum ggml_type */
+    void *buffer;
+    int64_t ne[4];
+    size_t nb[4];
+    int op;                                    /* never read by the adapter */
+    int32_t op_params[64 / sizeof(int32_t)];
+    int32_t flags;
+    struct ggml_tensor *src[MOCK_MAX_SRC];
+    struct ggml_tensor *view_src;
+    size_t view_offs;
+    void *data;
+    char name[64];
+    void *extra;
+};
+
+#include "mxfa_ggml.h"
+
+static void set4(int64_t *ne, int64_t a, int64_t b, int64_t c, int64_t d) { ne[0] = a; ne[1] = b; ne[2] = c; ne[3] = d; }
+
+static void contig(struct ggml_tensor *t, size_t esz) {
+    t->nb[0] = esz;
+    for (int i = 1; i < 4; i++) t->nb[i] = t->nb[i - 1] * (size_t)t->ne[i - 1];
+}
+
+static void show(const char *name, const mxfa_tensor *d) {
+    if (!d) { printf("%s NULL\n", name); return; }
+    printf("%s type=%d ne=%lld,%lld,%lld,%lld nb=%zu,%zu,%zu,%zu data=%p\n", name, d->type,
+           (long long)d->ne[0], (long long)d->ne[1], (long long)d->ne[2], (long long)d->ne[3],
+           d->nb[0], d->nb[1], d->nb[2], d->nb[3], d->data);
+}
+
+int main(int argc, char **argv) {
+    const int with_mask = argc > 1 && strcmp(argv[1], "mask") == 0;
+    const int with_sinks = argc > 1 && strcmp(argv[1], "sinks") == 0;
+    struct ggml_tensor q, k, v, m, node, sinks;
+    memset(&q, 0, sizeof q); memset(&k, 0, sizeof k); memset(&v, 0, sizeof v);
+    memset(&m, 0, sizeof m); memset(&node, 0, sizeof node); memset(&sinks, 0, sizeof sinks);
+    /* batched CFG decode view (src/qwen3-lm.h:780-794): q [128,1,32,8] permuted,
+     * k/v [128, 8192, 8, 8] F16 cache views, mask [8192, 1, 1, 8] F16 */
+    q.type = 0; set4(q.ne, 128, 1, 32, 8); q.nb[0] = 4; q.nb[1] = 4 * 128 * 32; q.nb[2] = 4 * 128; q.nb[3] = 4 * 128 * 32;
+    q.data = (void *)(uintptr_t)0x100000;
+    k.type = 1; set4(k.ne, 128, 8192, 8, 8); k.nb[0] = 2; k.nb[1] = 256; k.nb[2] = 256 * 8192; k.nb[3] = 256 * 8192 * 8;
+    k.data = (void *)(uintptr_t)0x200000;
+    v = k; v.data = (void *)(uintptr_t)0x300000;
+    m.type = 1; set4(m.ne, 8192, 1, 1, 8); contig(&m, 2); m.data = (void *)(uintptr_t)0x400000;
+    node.type = 0; set4(node.ne, 128, 32, 1, 8); contig(&node, 4); node.data = (void *)(uintptr_t)0x500000;
+    node.op = 12345;   /* arbitrary: the adapter does not look at it */
+    node.src[0] = &q; node.src[1] = &k; node.src[2] = &v; node.src[3] = with_mask ? &m : NULL;
+    if (with_sinks) node.src[4] = &sinks;
+    const float params[3] = {0.08838834764831845f, 0.0f, 0.0f};
+    const int32_t prec = 10;   /* GGML_PREC_F32 */
+    memcpy(node.op_params, params, sizeof params);
+    memcpy((char *)node.op_params + 3 * sizeof(float), &prec, sizeof prec);
+
+    mxfa_tensor dq, dk, dv, dm, dd;
+    const mxfa_tensor *mp = NULL;
+    mxfa_params p;
+    const int rc = mxfa_ggml_unpack(&node, &dq, &dk, &dv, &dm, &mp, &dd, &p);
+    printf("unpack %d\n", rc);
+    if (rc == 0) {
+        show("q", &dq); show("k", &dk); show("v", &dv); show("mask", mp); show("dst", &dd);
+        printf("params scale=%.9g max_bias=%g softcap=%g prec=%d\n", p.scale, p.max_bias, p.logit_softcap, p.prec);
+    }
+    printf("supports %d\n", mxfa_ggml_supports(&node));
+    return 0;
+}
