@@ -33,6 +33,8 @@
 // element).  The causal prefill mask thus costs half the work of the dense
 // problem and no per-element mask traffic below the diagonal.
 
+#include <type_traits>
+
 #include "mxfa_common.h"
 #include "mxfa_internal.h"
 
@@ -99,6 +101,29 @@ struct TileClasses {
     }
 };
 
+// Direct HBM -> LDS copy of 16 bytes per lane from a wave-uniform base plus
+// a per-lane 32-bit byte offset (lane l's bytes land at lds_base + 16*l).
+__device__ __forceinline__ void dma16_so(const char *sbase, uint32_t voff, void *lds_base) {
+    const uint32_t lds_addr = (uint32_t)(uintptr_t)(lds_void *)lds_base;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(sbase)
+                 : "memory", "m0");
+}
+
+// Max of a lane's value and the same register of lane l ^ 32 (one
+// v_permlane32_swap: lanes l and l ^ 32 hold the two key halves of a query).
+__device__ __forceinline__ float max_pair32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                    false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float sum_pair32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                    false, false);
+    return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+
 template <int T>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fa_prefill_kernel(const FaArgs a) {
@@ -108,7 +133,8 @@ fa_prefill_kernel(const FaArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, h = lane >> 5;
     const int qt = gridDim.x - 1 - blockIdx.x;   // longest (causal) tiles first
     const int head = blockIdx.y, b = blockIdx.z;
@@ -137,7 +163,7 @@ fa_prefill_kernel(const FaArgs a) {
     TileClasses tc{0u, 0u, a.tile_class != nullptr};
     if (tc.present) {
         const uint32_t *row = (const uint32_t *)(a.tile_class + ((int64_t)plane * a.n_qt + qt) * a.n_kt_pad);
-        const int lane4 = 4 * (tid & 63);
+        const int lane4 = 4 * lane;
         if (lane4 < a.n_kt) tc.w0 = row[lane4 >> 2];
         if (256 + lane4 < a.n_kt) tc.w1 = row[(256 + lane4) >> 2];
     }
@@ -149,6 +175,8 @@ fa_prefill_kernel(const FaArgs a) {
     const float sl2 = a.scale * kLog2e;
     const bool use_softcap = a.softcap != 0.0f;
     const float sc_in = use_softcap ? a.scale / a.softcap : 0.0f;
+    // the lean path takes max over raw scores, valid for a positive scale
+    const bool lean_ok = !use_softcap && sl2 > 0.0f;
 
     const char *kbase = a.k + (int64_t)kvh * a.k_nb2 + (int64_t)bk * a.k_nb3;
     const char *vbase = a.v + (int64_t)kvh * a.v_nb2 + (int64_t)bk * a.v_nb3;
@@ -160,70 +188,106 @@ fa_prefill_kernel(const FaArgs a) {
         for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
     float m2 = -INFINITY, lsum = 0.0f;
 
-    // Tile staging: each wave DMAs 16 keys of K and of V (4 instructions of
-    // 4 keys x 16 chunks); lane -> (key 4j + lane/16, slot lane%16), and the
-    // slot holds the swizzled logical chunk.  Keys past Skv re-read row
-    // Skv-1 (in bounds; their scores are forced to -inf).
+    // Tile staging: each wave DMAs keys 16w..16w+15 of K and of V (4
+    // instructions of 4 keys x 16 chunks); lane -> (key 4j + lane/16, slot
+    // lane%16), the slot holding the swizzled logical chunk.  Row 4j + dk
+    // (dk = lane/16) of the wave's 16 comes from the wave-uniform base
+    // tile + (16w + 4j) rows plus a per-lane offset dk * nb1 + 16 * chunk.
+    // With swz_k(k) = k & 15 the chunk is (slot ^ dk) ^ 4j, and with swz_v
+    // it is (slot ^ swz_v(dk)) ^ 2(j & 1): when nb1 is a multiple of 256 the
+    // offset is one register XOR a per-j constant.  The last, partial tile
+    // clamps keys to Skv - 1.
     const int dma_key = lane >> 4, dma_slot = lane & 15;
+    const bool nb_fast = (a.k_nb1 % 256 == 0) && (a.v_nb1 % 256 == 0);
+    const uint32_t xk = (uint32_t)(dma_key * a.k_nb1) | (16u * (uint32_t)(dma_slot ^ dma_key));
+    const uint32_t xv = (uint32_t)(dma_key * a.v_nb1) | (16u * (uint32_t)(dma_slot ^ swz_v(dma_key)));
     auto issue = [&](int kt, int stage) {
         uint8_t *ks = smem + stage * kStageBytes;
         uint8_t *vs = ks + kTileBytes;
         const int key0 = kt * kPfBN;
+        if (key0 + kPfBN <= a.Skv && nb_fast) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int krow = 16 * wave + 4 * j + dma_key;
-            const int key = min(key0 + krow, a.Skv - 1);
-            dma16(kbase + (int64_t)key * a.k_nb1 + 16 * (dma_slot ^ swz_k(krow)), ks + (16 * wave + 4 * j) * 256);
-            dma16(vbase + (int64_t)key * a.v_nb1 + 16 * (dma_slot ^ swz_v(krow)), vs + (16 * wave + 4 * j) * 256);
+            for (int j = 0; j < 4; j++) {
+                const int r0 = key0 + 16 * wave + 4 * j;
+                dma16_so(kbase + (int64_t)r0 * a.k_nb1, xk ^ (64u * j), ks + (16 * wave + 4 * j) * 256);
+                dma16_so(vbase + (int64_t)r0 * a.v_nb1, xv ^ (32u * (j & 1)), vs + (16 * wave + 4 * j) * 256);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int krow = 16 * wave + 4 * j + dma_key;
+                const int kr = min(key0 + krow, a.Skv - 1);
+                dma16(kbase + (int64_t)kr * a.k_nb1 + 16 * (dma_slot ^ swz_k(krow)), ks + (16 * wave + 4 * j) * 256);
+                dma16(vbase + (int64_t)kr * a.v_nb1 + 16 * (dma_slot ^ swz_v(krow)), vs + (16 * wave + 4 * j) * 256);
+            }
         }
     };
 
-    // transpose-read geometry of the V^T operand (see lds_read_tr16)
-    const int trg = lane >> 4, tri = lane & 15;
-    const int tr_h = trg >> 1, tr_ds = trg & 1;
+    // LDS read geometry.  K operand of dim-step t for keys 32kb + l32:
+    // chunk (2t + h) ^ (l32 & 15) of row l32 (+ kb * 32 rows).  V^T operand
+    // (transpose reads) of dim tile dt for keys 16ks + 8u + tr_key:
+    // chunk (4dt + c0) ^ swz_v(tr_key) of that row.
+    uint32_t kaddr[8], vaddr[4];
+#pragma unroll
+    for (int t = 0; t < 8; t++) kaddr[t] = l32 * 256 + 16 * ((2 * t + h) ^ (l32 & 15));
+    {
+        const int trg = lane >> 4, tri = lane & 15;
+        const int tr_key = 4 * (trg >> 1) + (tri >> 2);
+        const int c0 = 2 * (trg & 1) + ((tri & 3) >> 1);
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+            vaddr[dt] = tr_key * 256 + 16 * ((4 * dt + c0) ^ swz_v(tr_key)) + 8 * (tri & 1);
+    }
 
-    const int n_kt = a.n_kt;
-    int kt = tc.next_live(0, n_kt);
-    if (kt < n_kt) issue(kt, 0);
-    int stage = 0;
-    while (kt < n_kt) {
-        const int kn = tc.next_live(kt + 1, n_kt);
-        if (kn < n_kt) {
-            issue(kn, stage ^ 1);
-            MXFA_WAIT_VMCNT(8);      // this tile's 8 copies done, next tile's in flight
-        } else {
-            MXFA_WAIT_VMCNT(0);
-        }
-        __builtin_amdgcn_s_barrier();
-        const int cl = tc.at(kt);
-        const uint8_t *ks = smem + stage * kStageBytes;
+    // One key tile.  STAGE is compile time so every LDS address is a
+    // register plus an immediate.
+    auto tile = [&](auto stage_c, int kt) {
+        constexpr int ST = decltype(stage_c)::value;
+        const uint8_t *ks = smem + ST * kStageBytes;
         const uint8_t *vs = ks + kTileBytes;
+        const int cl = tc.at(kt);
         const int key0 = kt * kPfBN;
         const bool tail = key0 + kPfBN > a.Skv;
-        const bool general = cl == 2 || tail || use_softcap;
+        const bool general = cl == 2 || tail || !lean_ok;
 
-        // S^T = K . Q^T for the two 32-key halves (independent MFMA chains).
-        // lane: query l32, keys 32kb + 8(r/4) + 4h + r%4
+        // S^T = K . Q^T for the two 32-key halves (independent MFMA chains),
+        // K operands read two steps ahead of their MFMA.
         f32x16 s[2];
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
             for (int r = 0; r < 16; r++) s[kb][r] = 0.0f;
+        u16x8 ka[2][3];   // rolling window: dim-steps t, t+1, t+2
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++) ka[kb][t] = *(const u16x8 *)(ks + kaddr[t] + kb * 32 * 256);
 #pragma unroll
         for (int t = 0; t < 8; t++) {
+            if (t + 2 < 8) {
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++) {
-                const int key = 32 * kb + l32;
-                const u16x8 av = *(const u16x8 *)(ks + key * 256 + 16 * ((2 * t + h) ^ swz_k(key)));
-                s[kb] = MF::run(__builtin_bit_cast(V8, av), qb[t], s[kb]);
+                for (int kb = 0; kb < 2; kb++)
+                    ka[kb][(t + 2) % 3] = *(const u16x8 *)(ks + kaddr[t + 2] + kb * 32 * 256);
             }
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++) s[kb] = MF::run(__builtin_bit_cast(V8, ka[kb][t % 3]), qb[t], s[kb]);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // scores -> exp2 domain
+
+        // scores -> probabilities (exp2 domain).  lane: query l32, keys
+        // 32kb + 8(r/4) + 4h + r%4.
+        // Row max of the tile.  Lean tiles (all-zero mask, full, no softcap,
+        // positive scale) take it on the raw scores; general tiles first
+        // form x = scale*s (+ softcap) + slope*mask in the exp2 domain, with
+        // -inf for masked and out-of-range keys.
+        float bmax;
         if (!general) {
+            float mx = -INFINITY;
 #pragma unroll
             for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) s[kb][r] *= sl2;
+                for (int r = 0; r < 16; r += 2) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s[kb][r], s[kb][r + 1]));
+            bmax = max_pair32(mx) * sl2;
         } else {
 #pragma unroll
             for (int kb = 0; kb < 2; kb++)
@@ -252,26 +316,37 @@ fa_prefill_kernel(const FaArgs a) {
                         s[kb][r] = xv;
                     }
                 }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[kb][r]);
+            bmax = max_pair32(mx);
         }
-        float bmax = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) bmax = fmaxf(bmax, s[kb][r]);
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-        // Lazy rescale: the reference max m2 is raised only when some row's
-        // new max exceeds it by more than 8 (exp2 domain), so p <= 2^8 and
-        // O, l are rescaled on few tiles.  O and l always share the same
-        // reference, so the softmax is unchanged.
+        // Lazy rescale (one place for both paths, so O is rescaled in
+        // place): the reference max m2 is raised only when some row's new
+        // max exceeds it by more than 8 (exp2 domain), so p <= 2^8.  O and l
+        // always share the reference, so the softmax is unchanged.
         if (__any(bmax > m2 + 8.0f)) {
             const float mnew = fmaxf(m2, bmax);
-            const float alpha = (mnew == -INFINITY) ? 1.0f : fast_exp2(m2 - mnew);
+            const float alpha = (mnew == -INFINITY || m2 == -INFINITY) ? 1.0f : fast_exp2(m2 - mnew);
             m2 = mnew;
             lsum *= alpha;
 #pragma unroll
             for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
         }
-        const float m_use = (m2 == -INFINITY) ? 0.0f : m2;
+        const float mneg = (m2 == -INFINITY) ? 0.0f : -m2;
+        if (!general) {
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) s[kb][r] = fast_exp2(fmaf(s[kb][r], sl2, mneg));
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) s[kb][r] = fast_exp2(s[kb][r] + mneg);   // exp2(-inf) = 0
+        }
         // P^T operands of the four 16-key steps ks:
         // k-slot 4u+i <-> key 16ks + 8u + 4h + i = register 8(ks&1) + 4u + i of s[ks>>1].
         // The row sum adds exactly the rounded values the MFMA consumes.
@@ -279,43 +354,57 @@ fa_prefill_kernel(const FaArgs a) {
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             const int kb = ks >> 1, rb = 8 * (ks & 1);
-            f32x4 lo, hi;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                lo[i] = fast_exp2(s[kb][rb + i] - m_use);       // exp2(-inf) = 0
-                hi[i] = fast_exp2(s[kb][rb + 4 + i] - m_use);
-            }
-            const u16x8 bits = cvt8<T>(lo, hi);
+            const u16x8 bits = cvt8<T>(f32x4{s[kb][rb], s[kb][rb + 1], s[kb][rb + 2], s[kb][rb + 3]},
+                                       f32x4{s[kb][rb + 4], s[kb][rb + 5], s[kb][rb + 6], s[kb][rb + 7]});
             lsum = sum8<T>(bits, lsum);
             pb[ks] = __builtin_bit_cast(V8, bits);
         }
         // O^T += V^T . P^T; the V^T operand comes from two transpose reads of
-        // the row-major V tile (keys 16ks + 8u + 4h + e, dims 32dt + l32).
+        // the row-major V tile (keys 16ks + 8u + tr_key, dims 32dt + l32).
+        // operands read three MFMAs ahead (rolling window of 4)
+        u16x8 va[4];
+        auto vread = [&](int i) {
+            const int dt = i >> 2, ks = i & 3;
+            const u16x4 p0 = lds_read_tr16(vs + vaddr[dt] + (16 * ks) * 256);
+            const u16x4 p1 = lds_read_tr16(vs + vaddr[dt] + (16 * ks + 8) * 256);
+            return u16x8{p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
+        };
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
+        for (int i = 0; i < 3; i++) va[i] = vread(i);
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                u16x4 part[2];
-#pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const int key = 16 * ks + 8 * u + 4 * tr_h + (tri >> 2);
-                    const int c = 4 * dt + 2 * tr_ds + ((tri & 3) >> 1);
-                    part[u] = lds_read_tr16(vs + key * 256 + 16 * (c ^ swz_v(key)) + 8 * (tri & 1));
-                }
-                const u16x8 av = {part[0][0], part[0][1], part[0][2], part[0][3],
-                                  part[1][0], part[1][1], part[1][2], part[1][3]};
-                o[dt] = MF::run(__builtin_bit_cast(V8, av), pb[ks], o[dt]);
-            }
+        for (int i = 0; i < 16; i++) {
+            if (i + 3 < 16) va[(i + 3) & 3] = vread(i + 3);
+            o[i >> 2] = MF::run(__builtin_bit_cast(V8, va[i & 3]), pb[i & 3], o[i >> 2]);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // every LDS read of this stage has returned before anyone refills it
-        MXFA_WAIT_LGKMCNT0();
-        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Double-buffered loop over the live tiles.  Per tile: wait for this
+    // wave's copies of the tile, one barrier (every wave's copies have
+    // landed and every wave is done with the other stage), issue the next
+    // tile into the other stage, compute.
+    const int n_kt = a.n_kt;
+    int kt = tc.next_live(0, n_kt);
+    if (kt < n_kt) issue(kt, 0);
+    std::integral_constant<int, 0> st0;
+    std::integral_constant<int, 1> st1;
+    while (kt < n_kt) {
+        int kn = tc.next_live(kt + 1, n_kt);
+        MXFA_WAIT_VMCNT(0);
         __builtin_amdgcn_s_barrier();
-        stage ^= 1;
+        if (kn < n_kt) issue(kn, 1);
+        tile(st0, kt);
+        kt = kn;
+        if (kt >= n_kt) break;
+        kn = tc.next_live(kt + 1, n_kt);
+        MXFA_WAIT_VMCNT(0);
+        __builtin_amdgcn_s_barrier();
+        if (kn < n_kt) issue(kn, 0);
+        tile(st1, kt);
         kt = kn;
     }
 
-    lsum += __shfl_xor(lsum, 32);
+    lsum = sum_pair32(lsum);
     if (!row_ok) return;
     const float inv = (lsum == 0.0f) ? 0.0f : 1.0f / lsum;
     float *dp = a.dst + (((int64_t)b * a.Sq + qrow) * a.Nh + head) * kD;
