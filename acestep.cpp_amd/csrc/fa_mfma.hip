@@ -105,9 +105,17 @@ struct TileClasses {
 // a per-lane 32-bit byte offset (lane l's bytes land at lds_base + 16*l).
 __device__ __forceinline__ void dma16_so(const char *sbase, uint32_t voff, void *lds_base) {
     const uint32_t lds_addr = (uint32_t)(uintptr_t)(lds_void *)lds_base;
+    // the base is wave-uniform by contract; readfirstlane lets the compiler
+    // see that too, so the "s" operand never lands in a VGPR pair
+    const uint64_t b = (uint64_t)(uintptr_t)sbase;
+    // (readfirstlane returns int: go through uint32_t so the low half is
+    // zero-extended, never sign-extended into the high half)
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
                  :
-                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(sbase)
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(sb)
                  : "memory", "m0");
 }
 
@@ -363,8 +371,9 @@ fa_prefill_kernel(const FaArgs a) {
         // the row-major V tile (keys 16ks + 8u + tr_key, dims 32dt + l32).
         // operands read three MFMAs ahead (rolling window of 4)
         u16x8 va[4];
+        // MFMA i = 4ks + dt: consecutive MFMAs go to different accumulators
         auto vread = [&](int i) {
-            const int dt = i >> 2, ks = i & 3;
+            const int dt = i & 3, ks = i >> 2;
             const u16x4 p0 = lds_read_tr16(vs + vaddr[dt] + (16 * ks) * 256);
             const u16x4 p1 = lds_read_tr16(vs + vaddr[dt] + (16 * ks + 8) * 256);
             return u16x8{p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
@@ -374,7 +383,7 @@ fa_prefill_kernel(const FaArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             if (i + 3 < 16) va[(i + 3) & 3] = vread(i + 3);
-            o[i >> 2] = MF::run(__builtin_bit_cast(V8, va[i & 3]), pb[i & 3], o[i >> 2]);
+            o[i & 3] = MF::run(__builtin_bit_cast(V8, va[i & 3]), pb[i >> 2], o[i & 3]);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
