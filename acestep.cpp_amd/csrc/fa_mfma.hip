@@ -41,8 +41,8 @@
 
 namespace mxfa {
 
-constexpr int kTileBytes = 16384;            // one K or one V^T tile
-constexpr int kStageBytes = 2 * kTileBytes;  // K + V^T
+constexpr int kTileBytes = 16384;            // K or V rows of one 64-key tile
+constexpr int kStageBytes = 2 * kTileBytes;  // K + V
 constexpr int kPfLds = 2 * kStageBytes;      // double buffered: 64 KB
 
 __global__ void __launch_bounds__(256) mask_classify_kernel(const FaArgs a, uint8_t *cls) {
@@ -94,28 +94,35 @@ struct TileClasses {
                                     : __builtin_amdgcn_readlane(w1, ((kt - 256) >> 2) & 63);
         return (int)((w >> (8 * (kt & 3))) & 0xFFu);
     }
+    // (readfirstlane: the result is wave-uniform, and the compiler must
+    // know it to keep the tile loop on scalar branches)
     __device__ __forceinline__ int next_live(int kt, int n) const {
         if (!present) return kt;
         while (kt < n && at(kt) == 0) kt++;
-        return kt;
+        return __builtin_amdgcn_readfirstlane(kt);
     }
 };
 
-// Direct HBM -> LDS copy of 16 bytes per lane from a wave-uniform base plus
-// a per-lane 32-bit byte offset (lane l's bytes land at lds_base + 16*l).
-__device__ __forceinline__ void dma16_so(const char *sbase, uint32_t voff, void *lds_base) {
-    const uint32_t lds_addr = (uint32_t)(uintptr_t)(lds_void *)lds_base;
-    // the base is wave-uniform by contract; readfirstlane lets the compiler
-    // see that too, so the "s" operand never lands in a VGPR pair
-    const uint64_t b = (uint64_t)(uintptr_t)sbase;
-    // (readfirstlane returns int: go through uint32_t so the low half is
-    // zero-extended, never sign-extended into the high half)
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
-    const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+// Buffer resource over `bytes` bytes from `base`, offset addressed (stride
+// 0): a load at or past `bytes` returns zeros and touches no memory.
+__device__ __forceinline__ i32x4 buf_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    i32x4 r;
+    r[0] = (int)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    r[1] = (int)((uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) & 0xFFFFu);
+    r[2] = (int)__builtin_amdgcn_readfirstlane(bytes);
+    r[3] = 0x00020000;   // 32-bit data format, no swizzle, no stride
+    return r;
+}
+
+// HBM -> LDS copy of 16 bytes per lane through a buffer resource: lane l
+// reads base + soff + voff(l) and its bytes land at LDS address
+// lds_addr + 16*l.  Same wait contract as dma16 (callers wait with
+// MXFA_WAIT_VMCNT before reading the buffer).
+__device__ __forceinline__ void dma16_buf(const i32x4 &rsrc, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  :
-                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(sb)
+                 : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
                  : "memory", "m0");
 }
 
@@ -132,6 +139,38 @@ __device__ __forceinline__ float sum_pair32(float x) {
     return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
+// acc *= alpha for a 16-register MFMA accumulator that stays in the
+// accumulation registers (AGPRs): read, multiply, write back in place.  The
+// O accumulators are only touched by the MFMAs and by this rare rescale, so
+// they never move between register files.
+__device__ __forceinline__ void scale_acc(f32x16 &o, float alpha) {
+    float t;
+    asm volatile(
+        "v_accvgpr_read_b32 %[t], %0\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %0, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %1\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %1, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %2\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %2, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %3\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %3, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %4\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %4, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %5\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %5, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %6\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %6, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %7\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %7, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %8\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %8, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %9\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %9, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %10\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %10, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %11\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %11, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %12\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %12, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %13\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %13, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %14\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %14, %[t]\n\t"
+        "v_accvgpr_read_b32 %[t], %15\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %15, %[t]"
+        : "+a"(o[0]), "+a"(o[1]), "+a"(o[2]), "+a"(o[3]), "+a"(o[4]), "+a"(o[5]), "+a"(o[6]), "+a"(o[7]),
+          "+a"(o[8]), "+a"(o[9]), "+a"(o[10]), "+a"(o[11]), "+a"(o[12]), "+a"(o[13]), "+a"(o[14]), "+a"(o[15]),
+          [t] "=&v"(t)
+        : [al] "v"(alpha));
+}
+
+// sched_group_barrier classes
+enum : int { kSgMfma = 0x008, kSgValu = 0x402, kSgDsRead = 0x100 };
+
 template <int T>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fa_prefill_kernel(const FaArgs a) {
@@ -140,12 +179,13 @@ fa_prefill_kernel(const FaArgs a) {
     static_assert(kD == 128, "kernel is written for D = 128");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
-    const int tid = threadIdx.x;
+    // (work-item / group ids through the intrinsics: always inline, scalar)
+    const int tid = (int)__builtin_amdgcn_workitem_id_x();
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, h = lane >> 5;
-    const int qt = gridDim.x - 1 - blockIdx.x;   // longest (causal) tiles first
-    const int head = blockIdx.y, b = blockIdx.z;
+    const int qt = a.n_qt - 1 - (int)__builtin_amdgcn_workgroup_id_x();   // longest (causal) tiles first
+    const int head = (int)__builtin_amdgcn_workgroup_id_y(), b = (int)__builtin_amdgcn_workgroup_id_z();
     const int kvh = head / a.G, bk = b / a.rk3;
     const int qrow = qt * kPfBM + wave * 32 + l32;
     const bool row_ok = qrow < a.Sq;
@@ -185,9 +225,69 @@ fa_prefill_kernel(const FaArgs a) {
     const float sc_in = use_softcap ? a.scale / a.softcap : 0.0f;
     // the lean path takes max over raw scores, valid for a positive scale
     const bool lean_ok = !use_softcap && sl2 > 0.0f;
+    const int n_kt = a.n_kt;
 
+    // K and V rows of this (batch, kv head) as buffer resources; rows past
+    // Skv (the partial last tile, and the look-ahead past the last tile)
+    // read as zeros.
     const char *kbase = a.k + (int64_t)kvh * a.k_nb2 + (int64_t)bk * a.k_nb3;
     const char *vbase = a.v + (int64_t)kvh * a.v_nb2 + (int64_t)bk * a.v_nb3;
+    const i32x4 rk = buf_rsrc(kbase, (uint32_t)((int64_t)(a.Skv - 1) * a.k_nb1 + 2 * kD));
+    const i32x4 rv = buf_rsrc(vbase, (uint32_t)((int64_t)(a.Skv - 1) * a.v_nb1 + 2 * kD));
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void *)smem);
+    const uint32_t k_row = (uint32_t)a.k_nb1, v_row = (uint32_t)a.v_nb1;
+
+    // Tile staging (double buffered, one 64-key tile per stage: K rows at
+    // +0, V rows at +16 KB, 256 B per key, 16-byte chunks XOR-swizzled).
+    // Wave w copies keys 16w..16w+15 of the tile (four copies of 4 keys x
+    // 16 chunks for K and for V): lane -> (key 16w + 4c + lane/16, slot
+    // lane%16), the slot holding the swizzled logical chunk, so the per-lane
+    // offset is a constant per copy c and the row offset a scalar.
+    const int dkey = lane >> 4, dslot = lane & 15;
+    uint32_t vk[4], vv[2];
+#pragma unroll
+    for (int c = 0; c < 4; c++) vk[c] = (uint32_t)dkey * k_row + 16u * (uint32_t)(dslot ^ swz_k(4 * c + dkey));
+#pragma unroll
+    for (int c = 0; c < 2; c++) vv[c] = (uint32_t)dkey * v_row + 16u * (uint32_t)(dslot ^ swz_v(4 * c + dkey));
+    auto issue = [&](int kt, auto st_c) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_c)::value;
+        const uint32_t r0 = (uint32_t)(kt * kPfBN + 16 * wave);
+        const uint32_t l0 = lds0 + ST * kStageBytes + (uint32_t)(16 * wave) * 256u;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            dma16_buf(rk, vk[c], (r0 + 4 * c) * k_row, l0 + 4 * c * 256);
+            dma16_buf(rv, vv[c & 1], (r0 + 4 * c) * v_row, l0 + kTileBytes + 4 * c * 256);
+        }
+    };
+
+    // LDS operand addresses.  QK: K operand of dim-step t for key l32 of a
+    // half: chunk (2t + h) ^ swz_k(l32) of row l32.  PV: V^T operand of dim
+    // tile dt for the 16-key step kk (keys 16kk + 8u + tr_key of a half):
+    // chunk (4dt + c0) ^ swz_v(tr_key) of that row, two transpose reads.
+    uint32_t kaddr[8], vaddr[4];
+#pragma unroll
+    for (int t = 0; t < 8; t++) kaddr[t] = l32 * 256 + 16 * ((2 * t + h) ^ swz_k(l32));
+    {
+        const int trg = lane >> 4, tri = lane & 15;
+        const int tr_key = 4 * (trg >> 1) + (tri >> 2);
+        const int c0 = 2 * (trg & 1) + ((tri >> 1) & 1);
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+            vaddr[dt] = tr_key * 256 + 16 * ((4 * dt + c0) ^ swz_v(tr_key)) + 8 * (tri & 1);
+    }
+    // K operand t of half p; V operand i = 4kk + dt of half p
+    auto kread = [&](auto st_c, int p, int t) __attribute__((always_inline)) -> u16x8 {
+        constexpr int ST = decltype(st_c)::value;
+        return *(const u16x8 *)(smem + ST * kStageBytes + p * 32 * 256 + kaddr[t]);
+    };
+    auto vread = [&](auto st_c, int p, int i) __attribute__((always_inline)) -> u16x8 {
+        constexpr int ST = decltype(st_c)::value;
+        const int dt = i & 3, kk = i >> 2;
+        const uint8_t *q = smem + ST * kStageBytes + kTileBytes + (32 * p + 16 * kk) * 256 + vaddr[dt];
+        const u16x4 p0 = lds_read_tr16(q);
+        const u16x4 p1 = lds_read_tr16(q + 8 * 256);
+        return u16x8{p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
+    };
 
     f32x16 o[4];
 #pragma unroll
@@ -196,235 +296,187 @@ fa_prefill_kernel(const FaArgs a) {
         for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
     float m2 = -INFINITY, lsum = 0.0f;
 
-    // Tile staging: each wave DMAs keys 16w..16w+15 of K and of V (4
-    // instructions of 4 keys x 16 chunks); lane -> (key 4j + lane/16, slot
-    // lane%16), the slot holding the swizzled logical chunk.  Row 4j + dk
-    // (dk = lane/16) of the wave's 16 comes from the wave-uniform base
-    // tile + (16w + 4j) rows plus a per-lane offset dk * nb1 + 16 * chunk.
-    // With swz_k(k) = k & 15 the chunk is (slot ^ dk) ^ 4j, and with swz_v
-    // it is (slot ^ swz_v(dk)) ^ 2(j & 1): when nb1 is a multiple of 256 the
-    // offset is one register XOR a per-j constant.  The last, partial tile
-    // clamps keys to Skv - 1.
-    const int dma_key = lane >> 4, dma_slot = lane & 15;
-    const bool nb_fast = (a.k_nb1 % 256 == 0) && (a.v_nb1 % 256 == 0);
-    const uint32_t xk = (uint32_t)(dma_key * a.k_nb1) | (16u * (uint32_t)(dma_slot ^ dma_key));
-    const uint32_t xv = (uint32_t)(dma_key * a.v_nb1) | (16u * (uint32_t)(dma_slot ^ swz_v(dma_key)));
-    auto issue = [&](int kt, int stage) {
-        uint8_t *ks = smem + stage * kStageBytes;
-        uint8_t *vs = ks + kTileBytes;
-        const int key0 = kt * kPfBN;
-        if (key0 + kPfBN <= a.Skv && nb_fast) {
+    // General tiles (mixed mask, tail, softcap, non-positive scale): replace
+    // the raw scores of a half by x = scale*s (+softcap) + slope*mask in the
+    // exp2 domain, -inf for masked and absent keys (lane: query l32, keys
+    // 8(r/4) + 4h + r%4 of the half).  Branch-free: the host routes here only
+    // masks whose rows hold at least round_up(Skv, 4) entries, so every
+    // 4-key group that starts below Skv is readable, and a group past Skv
+    // reads the last one instead.
+    const int mask_last4 = ((a.Skv + 3) & ~3) - 4;
+    auto general_x = [&](f32x16 &sc, int key0, int cl) __attribute__((always_inline)) {
+        float mv[16];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int r0 = key0 + 16 * wave + 4 * j;
-                dma16_so(kbase + (int64_t)r0 * a.k_nb1, xk ^ (64u * j), ks + (16 * wave + 4 * j) * 256);
-                dma16_so(vbase + (int64_t)r0 * a.v_nb1, xv ^ (32u * (j & 1)), vs + (16 * wave + 4 * j) * 256);
+        for (int j = 0; j < 4; j++) {
+            const int kb4 = key0 + 8 * j + 4 * h;
+#pragma unroll
+            for (int i = 0; i < 4; i++) mv[4 * j + i] = 0.0f;
+            if (cl == 2) {
+                const u16x4 mw = *(const u16x4 *)(mrow + min(kb4, mask_last4));
+#pragma unroll
+                for (int i = 0; i < 4; i++) mv[4 * j + i] = h2f_bits(mw[i]) * slope_l2;
             }
+        }
+        if (use_softcap) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) sc[r] = (a.softcap * fast_tanh(sc[r] * sc_in)) * kLog2e + mv[r];
         } else {
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int krow = 16 * wave + 4 * j + dma_key;
-                const int kr = min(key0 + krow, a.Skv - 1);
-                dma16(kbase + (int64_t)kr * a.k_nb1 + 16 * (dma_slot ^ swz_k(krow)), ks + (16 * wave + 4 * j) * 256);
-                dma16(vbase + (int64_t)kr * a.v_nb1 + 16 * (dma_slot ^ swz_v(krow)), vs + (16 * wave + 4 * j) * 256);
-            }
+            for (int r = 0; r < 16; r++) sc[r] = fmaf(sc[r], sl2, mv[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int key = key0 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (mv[r] == -INFINITY || key >= a.Skv) sc[r] = -INFINITY;
         }
     };
+    // probabilities of pair u (registers 2u, 2u+1) of a half, packed into
+    // the P^T operand: k-slot 4u' + i <-> key 16kk + 8u' + 4h + i =
+    // register 8kk + 4u' + i, i.e. operand kk holds registers 8kk..8kk+7
+    auto pair = [&](const f32x16 &sc, int u, float g, float mneg, u16x8 (&pw)[2]) __attribute__((always_inline)) {
+        const float p0 = fast_exp2(fmaf(sc[2 * u], g, mneg));
+        const float p1 = fast_exp2(fmaf(sc[2 * u + 1], g, mneg));
+        pw[u >> 2][2 * (u & 3)] = Mfma16<T>::from_f32(p0);
+        pw[u >> 2][2 * (u & 3) + 1] = Mfma16<T>::from_f32(p1);
+    };
+    auto half_max = [&](const f32x16 &sc) __attribute__((always_inline)) {
+        return fmaxf(fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                           fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7]))),
+                     fmaxf(fmaxf(fmaxf(sc[8], sc[9]), fmaxf(sc[10], sc[11])),
+                           fmaxf(fmaxf(sc[12], sc[13]), fmaxf(sc[14], sc[15]))));
+    };
 
-    // LDS read geometry.  K operand of dim-step t for keys 32kb + l32:
-    // chunk (2t + h) ^ (l32 & 15) of row l32 (+ kb * 32 rows).  V^T operand
-    // (transpose reads) of dim tile dt for keys 16ks + 8u + tr_key:
-    // chunk (4dt + c0) ^ swz_v(tr_key) of that row.
-    uint32_t kaddr[8], vaddr[4];
-#pragma unroll
-    for (int t = 0; t < 8; t++) kaddr[t] = l32 * 256 + 16 * ((2 * t + h) ^ (l32 & 15));
-    {
-        const int trg = lane >> 4, tri = lane & 15;
-        const int tr_key = 4 * (trg >> 1) + (tri >> 2);
-        const int c0 = 2 * (trg & 1) + ((tri & 3) >> 1);
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-            vaddr[dt] = tr_key * 256 + 16 * ((4 * dt + c0) ^ swz_v(tr_key)) + 8 * (tri & 1);
-    }
-
-    // One key tile.  STAGE is compile time so every LDS address is a
-    // register plus an immediate.
-    auto tile = [&](auto stage_c, int kt) {
-        constexpr int ST = decltype(stage_c)::value;
-        const uint8_t *ks = smem + ST * kStageBytes;
-        const uint8_t *vs = ks + kTileBytes;
-        const int cl = tc.at(kt);
+    // One 64-key tile, as two 32-key halves a (keys 0..31) and b:
+    //   R1  QK a                         (matrix cores)
+    //   R2  QK b       | softmax of a, speculative with the current
+    //                    reference max m2 (vector ALUs, interleaved)
+    //   R3  max of b; if some row's tile max exceeds m2 by more than 8
+    //       (exp2 domain), raise m2, rescale O and l, redo a  (rare)
+    //   R4  PV a       | softmax of b
+    //   R5  PV b
+    // The code is laid out in issue order; sched_barrier fences keep it.
+    // Operand reads run two MFMAs ahead.
+    auto tile = [&](auto st_c, int kt) __attribute__((always_inline)) {
+        const int cl = __builtin_amdgcn_readfirstlane(tc.at(kt));
         const int key0 = kt * kPfBN;
-        const bool tail = key0 + kPfBN > a.Skv;
-        const bool general = cl == 2 || tail || !lean_ok;
+        const bool general =
+            __builtin_amdgcn_readfirstlane((int)(cl == 2 || key0 + kPfBN > a.Skv || !lean_ok)) != 0;
+        const float g = general ? 1.0f : sl2;   // wave-uniform
+        f32x16 sa, sb;
+        u16x8 op[8];
 
-        // S^T = K . Q^T for the two 32-key halves (independent MFMA chains),
-        // K operands read two steps ahead of their MFMA.
-        f32x16 s[2];
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) s[kb][r] = 0.0f;
-        u16x8 ka[2][3];   // rolling window: dim-steps t, t+1, t+2
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++) ka[kb][t] = *(const u16x8 *)(ks + kaddr[t] + kb * 32 * 256);
+        // ---- R1: QK a ----
+        op[0] = kread(st_c, 0, 0);
+        op[1] = kread(st_c, 0, 1);
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            if (t + 2 < 8) {
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++)
-                    ka[kb][(t + 2) % 3] = *(const u16x8 *)(ks + kaddr[t + 2] + kb * 32 * 256);
-            }
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++) s[kb] = MF::run(__builtin_bit_cast(V8, ka[kb][t % 3]), qb[t], s[kb]);
+            if (t + 2 < 8) op[t + 2] = kread(st_c, 0, t + 2);
+            else op[t - 6] = kread(st_c, 1, t - 6);
+            sa = MF::run(__builtin_bit_cast(V8, op[t]), qb[t], t == 0 ? f32x16{} : sa);
             __builtin_amdgcn_sched_barrier(0);
         }
+        if (general) general_x(sa, key0, cl);
+        __builtin_amdgcn_sched_barrier(0);
 
-        // scores -> probabilities (exp2 domain).  lane: query l32, keys
-        // 32kb + 8(r/4) + 4h + r%4.
-        // Row max of the tile.  Lean tiles (all-zero mask, full, no softcap,
-        // positive scale) take it on the raw scores; general tiles first
-        // form x = scale*s (+ softcap) + slope*mask in the exp2 domain, with
-        // -inf for masked and out-of-range keys.
-        float bmax;
-        if (!general) {
-            float mx = -INFINITY;
+        // ---- R2: QK b | softmax a (speculative) ----
+        const float mneg0 = (m2 == -INFINITY) ? 0.0f : -m2;
+        float mxa = 0.0f;
+        u16x8 pa[2], pb[2];
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int r = 0; r < 16; r += 2) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s[kb][r], s[kb][r + 1]));
-            bmax = max_pair32(mx) * sl2;
-        } else {
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int kbase4 = key0 + 32 * kb + 8 * j + 4 * h;
-                    float mv[4] = {0.f, 0.f, 0.f, 0.f};
-                    if (cl == 2) {
-                        if (kbase4 + 3 < a.Skv) {
-                            const u16x4 mw = *(const u16x4 *)(mrow + kbase4);
-#pragma unroll
-                            for (int i = 0; i < 4; i++) mv[i] = h2f_bits(mw[i]) * slope_l2;
-                        } else {
-#pragma unroll
-                            for (int i = 0; i < 4; i++)
-                                mv[i] = (kbase4 + i < a.Skv) ? h2f_bits(mrow[kbase4 + i]) * slope_l2 : -INFINITY;
-                        }
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int r = 4 * j + i;
-                        float xv;
-                        if (use_softcap) xv = (a.softcap * tanhf(s[kb][r] * sc_in)) * kLog2e + mv[i];
-                        else xv = fmaf(s[kb][r], sl2, mv[i]);
-                        if (mv[i] == -INFINITY || kbase4 + i >= a.Skv) xv = -INFINITY;
-                        s[kb][r] = xv;
-                    }
-                }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[kb][r]);
-            bmax = max_pair32(mx);
+        for (int t = 0; t < 8; t++) {
+            if (t + 2 < 8) op[t + 2] = kread(st_c, 1, t + 2);
+            else op[t - 6] = vread(st_c, 0, t - 6);   // PV a operands 0, 1
+            sb = MF::run(__builtin_bit_cast(V8, op[t]), qb[t], t == 0 ? f32x16{} : sb);
+            if (t == 0) mxa = half_max(sa);
+            else pair(sa, t - 1, g, mneg0, pa);
+            if (t == 7) pair(sa, 7, g, mneg0, pa);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // Lazy rescale (one place for both paths, so O is rescaled in
-        // place): the reference max m2 is raised only when some row's new
-        // max exceeds it by more than 8 (exp2 domain), so p <= 2^8.  O and l
-        // always share the reference, so the softmax is unchanged.
-        if (__any(bmax > m2 + 8.0f)) {
+        float la = sum8<T>(pa[1], sum8<T>(pa[0], 0.0f));
+        // keep the speculative softmax here, overlapped with QK b (it is
+        // redone on the rare path, so it would otherwise sink past R3)
+        asm volatile("" ::"v"(pa[0]), "v"(pa[1]), "v"(la), "v"(mxa));
+        if (general) general_x(sb, key0 + 32, cl);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- R3: tile max, reference update (rare rescale) ----
+        const float bmax = max_pair32(fmaxf(mxa, half_max(sb))) * g;
+        const bool any_need = __builtin_amdgcn_ballot_w64(bmax > m2 + 8.0f) != 0;   // wave-uniform
+        if (any_need) {
             const float mnew = fmaxf(m2, bmax);
-            const float alpha = (mnew == -INFINITY || m2 == -INFINITY) ? 1.0f : fast_exp2(m2 - mnew);
+            const float alpha = (m2 == -INFINITY) ? 1.0f : fast_exp2(m2 - mnew);
             m2 = mnew;
             lsum *= alpha;
 #pragma unroll
             for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
+            const float mn = (m2 == -INFINITY) ? 0.0f : -m2;
+#pragma unroll
+            for (int u = 0; u < 8; u++) pair(sa, u, g, mn, pa);
+            la = sum8<T>(pa[1], sum8<T>(pa[0], 0.0f));
         }
         const float mneg = (m2 == -INFINITY) ? 0.0f : -m2;
-        if (!general) {
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- R4: PV a | softmax b ----
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) s[kb][r] = fast_exp2(fmaf(s[kb][r], sl2, mneg));
-        } else {
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) s[kb][r] = fast_exp2(s[kb][r] + mneg);   // exp2(-inf) = 0
-        }
-        // P^T operands of the four 16-key steps ks:
-        // k-slot 4u+i <-> key 16ks + 8u + 4h + i = register 8(ks&1) + 4u + i of s[ks>>1].
-        // The row sum adds exactly the rounded values the MFMA consumes.
-        V8 pb[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            const int kb = ks >> 1, rb = 8 * (ks & 1);
-            const u16x8 bits = cvt8<T>(f32x4{s[kb][rb], s[kb][rb + 1], s[kb][rb + 2], s[kb][rb + 3]},
-                                       f32x4{s[kb][rb + 4], s[kb][rb + 5], s[kb][rb + 6], s[kb][rb + 7]});
-            lsum = sum8<T>(bits, lsum);
-            pb[ks] = __builtin_bit_cast(V8, bits);
-        }
-        // O^T += V^T . P^T; the V^T operand comes from two transpose reads of
-        // the row-major V tile (keys 16ks + 8u + tr_key, dims 32dt + l32).
-        // operands read three MFMAs ahead (rolling window of 4)
-        u16x8 va[4];
-        // MFMA i = 4ks + dt: consecutive MFMAs go to different accumulators
-        auto vread = [&](int i) {
-            const int dt = i & 3, ks = i >> 2;
-            const u16x4 p0 = lds_read_tr16(vs + vaddr[dt] + (16 * ks) * 256);
-            const u16x4 p1 = lds_read_tr16(vs + vaddr[dt] + (16 * ks + 8) * 256);
-            return u16x8{p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
-        };
-#pragma unroll
-        for (int i = 0; i < 3; i++) va[i] = vread(i);
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            if (i + 3 < 16) va[(i + 3) & 3] = vread(i + 3);
-            o[i & 3] = MF::run(__builtin_bit_cast(V8, va[i & 3]), pb[i >> 2], o[i & 3]);
+        for (int i = 0; i < 8; i++) {
+            if (i + 2 < 8) op[(i + 2) & 7] = vread(st_c, 0, i + 2);
+            else op[(i + 2) & 7] = vread(st_c, 1, i - 6);   // PV b operands 0, 1
+            o[i & 3] = MF::run(__builtin_bit_cast(V8, op[i & 7]), __builtin_bit_cast(V8, pa[i >> 2]), o[i & 3]);
+            pair(sb, i, g, mneg, pb);
             __builtin_amdgcn_sched_barrier(0);
         }
+        const float lb = sum8<T>(pb[1], sum8<T>(pb[0], 0.0f));
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- R5: PV b ----
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (i + 2 < 8) op[(i + 2) & 7] = vread(st_c, 1, i + 2);
+            o[i & 3] = MF::run(__builtin_bit_cast(V8, op[i & 7]), __builtin_bit_cast(V8, pb[i >> 2]), o[i & 3]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        lsum += la + lb;
     };
 
     // Double-buffered loop over the live tiles.  Per tile: wait for this
     // wave's copies of the tile, one barrier (every wave's copies have
     // landed and every wave is done with the other stage), issue the next
-    // tile into the other stage, compute.
-    const int n_kt = a.n_kt;
-    int kt = tc.next_live(0, n_kt);
-    if (kt < n_kt) issue(kt, 0);
+    // live tile into the other stage, compute.  (No divergent early exits
+    // anywhere: they would put the tile loop under divergent control flow.)
     std::integral_constant<int, 0> st0;
     std::integral_constant<int, 1> st1;
+    int kt = tc.next_live(0, n_kt);
+    if (kt < n_kt) issue(kt, st0);
     while (kt < n_kt) {
         int kn = tc.next_live(kt + 1, n_kt);
         MXFA_WAIT_VMCNT(0);
         __builtin_amdgcn_s_barrier();
-        if (kn < n_kt) issue(kn, 1);
+        if (kn < n_kt) issue(kn, st1);
         tile(st0, kt);
         kt = kn;
         if (kt >= n_kt) break;
         kn = tc.next_live(kt + 1, n_kt);
         MXFA_WAIT_VMCNT(0);
         __builtin_amdgcn_s_barrier();
-        if (kn < n_kt) issue(kn, 0);
+        if (kn < n_kt) issue(kn, st0);
         tile(st1, kt);
         kt = kn;
     }
 
     lsum = sum_pair32(lsum);
-    if (!row_ok) return;
     const float inv = (lsum == 0.0f) ? 0.0f : 1.0f / lsum;
-    float *dp = a.dst + (((int64_t)b * a.Sq + qrow) * a.Nh + head) * kD;
+    float *dp = a.dst + (((int64_t)b * a.Sq + qrow_c) * a.Nh + head) * kD;
+    if (row_ok) {
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++)
+        for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int d0 = 32 * dt + 8 * j + 4 * h;
-            *(f32x4 *)(dp + d0) = f32x4{o[dt][4 * j] * inv, o[dt][4 * j + 1] * inv, o[dt][4 * j + 2] * inv,
-                                        o[dt][4 * j + 3] * inv};
-        }
+            for (int jj = 0; jj < 4; jj++) {
+                const int d0 = 32 * dt + 8 * jj + 4 * h;
+                *(f32x4 *)(dp + d0) = f32x4{o[dt][4 * jj] * inv, o[dt][4 * jj + 1] * inv,
+                                            o[dt][4 * jj + 2] * inv, o[dt][4 * jj + 3] * inv};
+            }
+    }
 }
 
 hipError_t launch_mask_classify(const FaArgs &a, int n_planes, uint8_t *classes, hipStream_t stream) {

@@ -194,10 +194,16 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     a.mask_al16 = mask_rows_aligned(16);
     a.mask_vec4 = a.mask_al8 && mask->ne[0] >= ((k->ne[1] + 3) & ~(int64_t)3);
     a.mask_vec16 = a.mask_vec4 && mask->ne[0] >= 16;
-    const bool mask_vec_ok = !mask || a.mask_al8;
+    // prefill: every 4-key mask group below Skv must be readable with one
+    // 8-byte load (rows 8-byte aligned, at least round_up(Skv, 4) entries)
+    const bool mask_vec_ok = !mask || a.mask_vec4;
     const int64_t n_kt = (a.Skv + kPfBN - 1) / kPfBN;
+    // the prefill kernel addresses one (batch, kv head)'s K and V rows with
+    // 32-bit offsets from a buffer base: every row of every key tile must
+    // lie within 4 GiB of it
+    const bool offsets_32 = (uint64_t)n_kt * kPfBN * (uint64_t)std::max(k->nb[1], v->nb[1]) <= 0xFFFFFFFFull;
     pl.prefill = (k->type == MXFA_TYPE_F16 || k->type == MXFA_TYPE_BF16) && a.Sq >= kPrefillMinSq && mask_vec_ok &&
-                 (!mask || n_kt <= kPfMaxKeyTiles);
+                 offsets_32 && (!mask || n_kt <= kPfMaxKeyTiles);
     if (pl.prefill) {
         a.n_qt = (a.Sq + kPfBM - 1) / kPfBM;
         a.n_kt = (int32_t)n_kt;

@@ -150,6 +150,15 @@ __device__ __forceinline__ float alibi_slope(const FaArgs &a, int h) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// tanh(x) = 1 - 2 / (e^(2x) + 1) with the hardware exp2 and reciprocal
+// (absolute error ~1e-7; saturates to +-1, e^(2x) = inf gives 1).  Inline
+// on purpose: a library call inside the attention loops costs a full
+// register save per call site.
+__device__ __forceinline__ float fast_tanh(float x) {
+    const float e = fast_exp2(x * (2.0f * kLog2e));
+    return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+}
+
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
 // lgkmcnt[11:8] | vmcnt[5:4] << 14).
 #define MXFA_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
