@@ -428,7 +428,7 @@ fa_decode_lds_kernel(const FaArgs a) {
     const char *vbase = a.v + (int64_t)t.kvh * a.v_nb2 + (int64_t)t.bk * a.v_nb3;
     const float sl2 = a.scale * kLog2e;
     const bool use_softcap = a.softcap != 0.0f;
-    const float sc_in = use_softcap ? a.scale / a.softcap : 0.0f;
+    const float sc_in = a.softcap_in;
     const int skv4 = (a.Skv + 3) & ~3;
     const int k0 = t.split * a.chunk;
     const int k1 = min(a.Skv, k0 + a.chunk);
@@ -676,7 +676,7 @@ fa_decode_reg_kernel(const FaArgs a) {
     const char *vbase = a.v + (int64_t)t.kvh * a.v_nb2 + (int64_t)t.bk * a.v_nb3;
     const float sl2 = a.scale * kLog2e;
     const bool use_softcap = a.softcap != 0.0f;
-    const float sc_in = use_softcap ? a.scale / a.softcap : 0.0f;
+    const float sc_in = a.softcap_in;
 
     const int k0 = t.split * a.chunk;
     const int k1 = min(a.Skv, k0 + a.chunk);

@@ -44,6 +44,7 @@ namespace mxfa {
 constexpr int kTileBytes = 16384;            // K or V rows of one 64-key tile
 constexpr int kStageBytes = 2 * kTileBytes;  // K + V
 constexpr int kPfLds = 2 * kStageBytes;      // double buffered: 64 KB
+constexpr uint32_t kXcds = 8;                // MI355X: workgroups go round-robin to 8 XCDs
 
 __global__ void __launch_bounds__(256) mask_classify_kernel(const FaArgs a, uint8_t *cls) {
     // One workgroup per (key tile, query tile, mask plane).  Each row of the
@@ -116,13 +117,14 @@ __device__ __forceinline__ i32x4 buf_rsrc(const void *base, uint32_t bytes) {
 }
 
 // HBM -> LDS copy of 16 bytes per lane through a buffer resource: lane l
-// reads base + soff + voff(l) and its bytes land at LDS address
+// reads base + voff(l) (zeros, and no memory access, when voff(l) + 16
+// exceeds the resource's size) and its bytes land at LDS address
 // lds_addr + 16*l.  Same wait contract as dma16 (callers wait with
 // MXFA_WAIT_VMCNT before reading the buffer).
-__device__ __forceinline__ void dma16_buf(const i32x4 &rsrc, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+__device__ __forceinline__ void dma16_buf(const i32x4 &rsrc, uint32_t voff, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                  :
-                 : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "s"(lds_addr), "v"(voff), "s"(rsrc)
                  : "memory", "m0");
 }
 
@@ -171,7 +173,9 @@ __device__ __forceinline__ void scale_acc(f32x16 &o, float alpha) {
 // sched_group_barrier classes
 enum : int { kSgMfma = 0x008, kSgValu = 0x402, kSgDsRead = 0x100 };
 
-template <int T>
+// CAP: logit softcap on (a per-call constant; its tanh path is compiled only
+// into the instances that need it, so it costs the common path no registers)
+template <int T, bool CAP>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fa_prefill_kernel(const FaArgs a) {
     using MF = Mfma32<T>;
@@ -184,8 +188,23 @@ fa_prefill_kernel(const FaArgs a) {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, h = lane >> 5;
-    const int qt = a.n_qt - 1 - (int)__builtin_amdgcn_workgroup_id_x();   // longest (causal) tiles first
-    const int head = (int)__builtin_amdgcn_workgroup_id_y(), b = (int)__builtin_amdgcn_workgroup_id_z();
+    // Job of this workgroup.  Workgroup ids go round-robin to the XCDs; each
+    // XCD gets a contiguous block of the job list, which is ordered by
+    // (batch, kv head), then by query tile from the last (longest under a
+    // causal mask) down, then by q head within the GQA group: the q tiles
+    // that share K/V rows run on one XCD and share its L2.
+    int qt, head, b;
+    {
+        const uint32_t L = __builtin_amdgcn_workgroup_id_x();
+        const uint32_t N = (uint32_t)(a.n_qt * a.Nh * a.B);
+        const uint32_t nq = N / kXcds, nr = N % kXcds, x = L % kXcds, s = L / kXcds;
+        const uint32_t J = x < nr ? x * (nq + 1) + s : nr * (nq + 1) + (x - nr) * nq + s;
+        const uint32_t per_u = (uint32_t)(a.G * a.n_qt);
+        const uint32_t u = J / per_u, r = J % per_u;
+        qt = __builtin_amdgcn_readfirstlane(a.n_qt - 1 - (int)(r / (uint32_t)a.G));
+        b = __builtin_amdgcn_readfirstlane((int)(u / (uint32_t)a.Nkv));
+        head = __builtin_amdgcn_readfirstlane((int)(u % (uint32_t)a.Nkv) * a.G + (int)(r % (uint32_t)a.G));
+    }
     const int kvh = head / a.G, bk = b / a.rk3;
     const int qrow = qt * kPfBM + wave * 32 + l32;
     const bool row_ok = qrow < a.Sq;
@@ -215,25 +234,27 @@ fa_prefill_kernel(const FaArgs a) {
         if (lane4 < a.n_kt) tc.w0 = row[lane4 >> 2];
         if (256 + lane4 < a.n_kt) tc.w1 = row[(256 + lane4) >> 2];
     }
-    const uint16_t *mrow =
-        a.mask ? (const uint16_t *)(a.mask + (int64_t)qrow_c * a.m_nb1 + (int64_t)(head % a.m_ne2) * a.m_nb2 +
-                                    (int64_t)(b % a.m_ne3) * a.m_nb3)
-               : nullptr;
+    // Mask rows of this (batch, head) plane through a buffer resource: lane
+    // offset qrow * nb1 + 2 * key (32-bit, the host checks the plane size);
+    // reads past the plane return zeros, so 4-key groups at the row end need
+    // no clamp (keys past Skv are masked anyway).
+    const char *mplane = a.mask ? a.mask + (int64_t)(head % a.m_ne2) * a.m_nb2 + (int64_t)(b % a.m_ne3) * a.m_nb3
+                                : a.q;
+    const __amdgpu_buffer_rsrc_t mrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)mplane, (short)0, a.mask ? (int)a.m_plane_bytes : 0, 0x00020000);
+    const uint32_t mrow_off = (uint32_t)qrow_c * (uint32_t)a.m_nb1 + 8u * (uint32_t)h;
     const float slope_l2 = alibi_slope(a, head) * kLog2e;
     const float sl2 = a.scale * kLog2e;
-    const bool use_softcap = a.softcap != 0.0f;
-    const float sc_in = use_softcap ? a.scale / a.softcap : 0.0f;
+    const float sc_in = a.softcap_in;
     // the lean path takes max over raw scores, valid for a positive scale
-    const bool lean_ok = !use_softcap && sl2 > 0.0f;
+    const bool lean_ok = !CAP && sl2 > 0.0f;
     const int n_kt = a.n_kt;
 
-    // K and V rows of this (batch, kv head) as buffer resources; rows past
-    // Skv (the partial last tile, and the look-ahead past the last tile)
-    // read as zeros.
+    // K and V rows of this (batch, kv head).
     const char *kbase = a.k + (int64_t)kvh * a.k_nb2 + (int64_t)bk * a.k_nb3;
     const char *vbase = a.v + (int64_t)kvh * a.v_nb2 + (int64_t)bk * a.v_nb3;
-    const i32x4 rk = buf_rsrc(kbase, (uint32_t)((int64_t)(a.Skv - 1) * a.k_nb1 + 2 * kD));
-    const i32x4 rv = buf_rsrc(vbase, (uint32_t)((int64_t)(a.Skv - 1) * a.v_nb1 + 2 * kD));
+    const uint64_t k_avail = (uint64_t)(a.Skv - 1) * (uint64_t)a.k_nb1 + 2 * kD;
+    const uint64_t v_avail = (uint64_t)(a.Skv - 1) * (uint64_t)a.v_nb1 + 2 * kD;
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void *)smem);
     const uint32_t k_row = (uint32_t)a.k_nb1, v_row = (uint32_t)a.v_nb1;
 
@@ -241,22 +262,34 @@ fa_prefill_kernel(const FaArgs a) {
     // +0, V rows at +16 KB, 256 B per key, 16-byte chunks XOR-swizzled).
     // Wave w copies keys 16w..16w+15 of the tile (four copies of 4 keys x
     // 16 chunks for K and for V): lane -> (key 16w + 4c + lane/16, slot
-    // lane%16), the slot holding the swizzled logical chunk, so the per-lane
-    // offset is a constant per copy c and the row offset a scalar.
+    // lane%16), the slot holding the swizzled logical chunk.  Each copy goes
+    // through a buffer resource based at the wave's first row and sized to
+    // the rows that exist, so keys past Skv (the last partial tile, and the
+    // look-ahead past the last tile) read as zeros and touch no memory.
     const int dkey = lane >> 4, dslot = lane & 15;
-    uint32_t vk[4], vv[2];
+    uint32_t vk[4], vv[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) vk[c] = (uint32_t)dkey * k_row + 16u * (uint32_t)(dslot ^ swz_k(4 * c + dkey));
-#pragma unroll
-    for (int c = 0; c < 2; c++) vv[c] = (uint32_t)dkey * v_row + 16u * (uint32_t)(dslot ^ swz_v(4 * c + dkey));
+    for (int c = 0; c < 4; c++) {
+        vk[c] = (uint32_t)(4 * c + dkey) * k_row + 16u * (uint32_t)(dslot ^ swz_k(4 * c + dkey));
+        vv[c] = (uint32_t)(4 * c + dkey) * v_row + 16u * (uint32_t)(dslot ^ swz_v(4 * c + dkey));
+    }
+    // (32-bit row offsets: the host routes here only (batch, kv head)
+    // slices whose key tiles lie within 4 GiB of their base; a look-ahead
+    // tile at or past n_kt gets an empty resource and reads nothing)
+    auto tile_rsrc = [&](const char *base, uint64_t avail, uint32_t row, int kt) __attribute__((always_inline)) {
+        const uint32_t off = (uint32_t)(kt * kPfBN + 16 * wave) * row;
+        const uint64_t n = kt < a.n_kt && avail > off ? min(avail - off, (uint64_t)0xFFFFFFFFu) : 0;
+        return buf_rsrc(base + off, (uint32_t)n);
+    };
     auto issue = [&](int kt, auto st_c) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_c)::value;
-        const uint32_t r0 = (uint32_t)(kt * kPfBN + 16 * wave);
         const uint32_t l0 = lds0 + ST * kStageBytes + (uint32_t)(16 * wave) * 256u;
+        const i32x4 rk = tile_rsrc(kbase, k_avail, k_row, kt);
+        const i32x4 rv = tile_rsrc(vbase, v_avail, v_row, kt);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            dma16_buf(rk, vk[c], (r0 + 4 * c) * k_row, l0 + 4 * c * 256);
-            dma16_buf(rv, vv[c & 1], (r0 + 4 * c) * v_row, l0 + kTileBytes + 4 * c * 256);
+            dma16_buf(rk, vk[c], l0 + 4 * c * 256);
+            dma16_buf(rv, vv[c], l0 + kTileBytes + 4 * c * 256);
         }
     };
 
@@ -296,38 +329,27 @@ fa_prefill_kernel(const FaArgs a) {
         for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
     float m2 = -INFINITY, lsum = 0.0f;
 
-    // General tiles (mixed mask, tail, softcap, non-positive scale): replace
-    // the raw scores of a half by x = scale*s (+softcap) + slope*mask in the
-    // exp2 domain, -inf for masked and absent keys (lane: query l32, keys
-    // 8(r/4) + 4h + r%4 of the half).  Branch-free: the host routes here only
-    // masks whose rows hold at least round_up(Skv, 4) entries, so every
-    // 4-key group that starts below Skv is readable, and a group past Skv
-    // reads the last one instead.
-    const int mask_last4 = ((a.Skv + 3) & ~3) - 4;
-    auto general_x = [&](f32x16 &sc, int key0, int cl) __attribute__((always_inline)) {
-        float mv[16];
+    // General tiles (mixed mask, tail, softcap, non-positive scale): the
+    // raw scores of a half become x = scale*s (+softcap) + slope*mask in the
+    // exp2 domain, -inf for masked keys and keys past Skv (lane: query l32,
+    // keys 8(r/4) + 4h + r%4 of the half).  The mask is read for every
+    // general tile: on a tile of class 1 it is all zero, and without a mask
+    // the resource is empty (reads return zero), so no branch is needed.
+    auto general_x = [&](f32x16 &sc, int key0) __attribute__((always_inline)) {
+        const int kmax = a.Skv - key0 - 4 * h;   // keys 8j + i >= kmax lie past Skv
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int kb4 = key0 + 8 * j + 4 * h;
+            const u16x4 mw = __builtin_bit_cast(
+                u16x4, __builtin_amdgcn_raw_buffer_load_b64(mrs, mrow_off + 2u * (uint32_t)key0 + 16u * j, 0, 0));
 #pragma unroll
-            for (int i = 0; i < 4; i++) mv[4 * j + i] = 0.0f;
-            if (cl == 2) {
-                const u16x4 mw = *(const u16x4 *)(mrow + min(kb4, mask_last4));
-#pragma unroll
-                for (int i = 0; i < 4; i++) mv[4 * j + i] = h2f_bits(mw[i]) * slope_l2;
+            for (int i = 0; i < 4; i++) {
+                const int r = 4 * j + i;
+                const float mv = h2f_bits(mw[i]) * slope_l2;
+                float x;
+                if constexpr (CAP) x = (a.softcap * fast_tanh(sc[r] * sc_in)) * kLog2e + mv;
+                else x = fmaf(sc[r], sl2, mv);
+                sc[r] = (mv == -INFINITY || 8 * j + i >= kmax) ? -INFINITY : x;
             }
-        }
-        if (use_softcap) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) sc[r] = (a.softcap * fast_tanh(sc[r] * sc_in)) * kLog2e + mv[r];
-        } else {
-#pragma unroll
-            for (int r = 0; r < 16; r++) sc[r] = fmaf(sc[r], sl2, mv[r]);
-        }
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int key = key0 + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (mv[r] == -INFINITY || key >= a.Skv) sc[r] = -INFINITY;
         }
     };
     // probabilities of pair u (registers 2u, 2u+1) of a half, packed into
@@ -375,7 +397,7 @@ fa_prefill_kernel(const FaArgs a) {
             sa = MF::run(__builtin_bit_cast(V8, op[t]), qb[t], t == 0 ? f32x16{} : sa);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (general) general_x(sa, key0, cl);
+        if (general) general_x(sa, key0);
         __builtin_amdgcn_sched_barrier(0);
 
         // ---- R2: QK b | softmax a (speculative) ----
@@ -396,7 +418,7 @@ fa_prefill_kernel(const FaArgs a) {
         // keep the speculative softmax here, overlapped with QK b (it is
         // redone on the rare path, so it would otherwise sink past R3)
         asm volatile("" ::"v"(pa[0]), "v"(pa[1]), "v"(la), "v"(mxa));
-        if (general) general_x(sb, key0 + 32, cl);
+        if (general) general_x(sb, key0 + 32);
         __builtin_amdgcn_sched_barrier(0);
 
         // ---- R3: tile max, reference update (rare rescale) ----
@@ -486,11 +508,14 @@ hipError_t launch_mask_classify(const FaArgs &a, int n_planes, uint8_t *classes,
 }
 
 hipError_t launch_fa_prefill(const FaArgs &a, int ktype, hipStream_t stream) {
-    dim3 grid(a.n_qt, a.Nh, a.B);
+    dim3 grid((uint32_t)a.n_qt * (uint32_t)a.Nh * (uint32_t)a.B);
+    const bool cap = a.softcap != 0.0f;
     if (ktype == T_F16) {
-        hipLaunchKernelGGL(fa_prefill_kernel<T_F16>, grid, dim3(256), kPfLds, stream, a);
+        if (cap) hipLaunchKernelGGL((fa_prefill_kernel<T_F16, true>), grid, dim3(256), kPfLds, stream, a);
+        else hipLaunchKernelGGL((fa_prefill_kernel<T_F16, false>), grid, dim3(256), kPfLds, stream, a);
     } else if (ktype == T_BF16) {
-        hipLaunchKernelGGL(fa_prefill_kernel<T_BF16>, grid, dim3(256), kPfLds, stream, a);
+        if (cap) hipLaunchKernelGGL((fa_prefill_kernel<T_BF16, true>), grid, dim3(256), kPfLds, stream, a);
+        else hipLaunchKernelGGL((fa_prefill_kernel<T_BF16, false>), grid, dim3(256), kPfLds, stream, a);
     } else {
         return hipErrorInvalidValue;
     }

@@ -182,8 +182,11 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     // ALiBi constants as ggml computes them (per-head slopes).
     const uint32_t n_head = (uint32_t)a.Nh;
     a.n_head_log2 = 1u << (uint32_t)std::floor(std::log2((double)n_head));
-    a.m0 = std::pow(2.0f, -(p->max_bias) / (float)a.n_head_log2);
-    a.m1 = std::pow(2.0f, -(p->max_bias / 2.0f) / (float)a.n_head_log2);
+    const float m0 = std::pow(2.0f, -(p->max_bias) / (float)a.n_head_log2);
+    const float m1 = std::pow(2.0f, -(p->max_bias / 2.0f) / (float)a.n_head_log2);
+    a.l2m0 = (float)std::log2((double)m0);
+    a.l2m1 = (float)std::log2((double)m1);
+    a.softcap_in = p->logit_softcap != 0.0f ? p->scale / p->logit_softcap : 0.0f;
     pl.ktype = k->type;
 
     auto mask_rows_aligned = [&](size_t al) {
@@ -194,9 +197,14 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     a.mask_al16 = mask_rows_aligned(16);
     a.mask_vec4 = a.mask_al8 && mask->ne[0] >= ((k->ne[1] + 3) & ~(int64_t)3);
     a.mask_vec16 = a.mask_vec4 && mask->ne[0] >= 16;
-    // prefill: every 4-key mask group below Skv must be readable with one
-    // 8-byte load (rows 8-byte aligned, at least round_up(Skv, 4) entries)
-    const bool mask_vec_ok = !mask || a.mask_vec4;
+    // prefill: mask rows are read in 8-byte groups of 4 keys (rows 8-byte
+    // aligned) through a buffer resource over one mask plane, addressed
+    // with 32-bit offsets
+    if (mask) {
+        const uint64_t plane = (uint64_t)(mask->ne[1] - 1) * mask->nb[1] + 2 * (uint64_t)mask->ne[0];
+        a.m_plane_bytes = plane <= 0x7FFFFFFFull ? (uint32_t)plane : 0;
+    }
+    const bool mask_vec_ok = !mask || (a.mask_al8 && a.m_plane_bytes != 0);
     const int64_t n_kt = (a.Skv + kPfBN - 1) / kPfBN;
     // the prefill kernel addresses one (batch, kv head)'s K and V rows with
     // 32-bit offsets from a buffer base: every row of every key tile must

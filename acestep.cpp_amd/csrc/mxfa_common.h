@@ -42,12 +42,14 @@ struct FaArgs {
     int32_t M;                            // rows per (b, kv head) = Sq*G
     int32_t row_tiles;                    // decode kernel: ceil(M/16)
     float scale, softcap;                 // softcap == 0: off
-    float max_bias, m0, m1;               // ALiBi (max_bias == 0: off)
+    float max_bias, l2m0, l2m1;           // ALiBi (max_bias == 0: off): log2 of ggml's m0, m1
+    float softcap_in;                     // scale / softcap (softcap != 0)
     uint32_t n_head_log2;
     // mask row alignment (8 / 16 bytes for every row start); mask_vec4:
     // 8-byte aligned rows holding at least round_up(Skv, 4) entries;
     // mask_vec16: the same with at least 16 entries (16-key DMA blocks)
     int32_t mask_al8, mask_al16, mask_vec4, mask_vec16;
+    uint32_t m_plane_bytes;               // prefill: bytes of one mask plane, (ne1 - 1) * nb1 + 2 * ne0
     // split-KV
     int32_t n_splits, chunk;
     float *part_o, *part_ml;
@@ -140,12 +142,15 @@ __device__ __forceinline__ float sum8(u16x8 p, float acc) {
     return acc;
 }
 
-// ALiBi slope of head h (ggml's formula; 1 when max_bias == 0).
+// ALiBi slope of head h (ggml's formula m0^(h+1), or m1^(2(h - n_head_log2)
+// + 1); 1 when max_bias == 0), as exp2(e * log2 m) with the host's log2 of
+// m0 and m1 (inline: a libm pow call would cost a register save per call
+// site).
 __device__ __forceinline__ float alibi_slope(const FaArgs &a, int h) {
     if (a.max_bias <= 0.0f) return 1.0f;
     const uint32_t hu = (uint32_t)h;
-    return hu < a.n_head_log2 ? powf(a.m0, (float)(hu + 1))
-                              : powf(a.m1, (float)(2 * (hu - a.n_head_log2) + 1));
+    return hu < a.n_head_log2 ? __builtin_amdgcn_exp2f(a.l2m0 * (float)(hu + 1))
+                              : __builtin_amdgcn_exp2f(a.l2m1 * (float)(2 * (hu - a.n_head_log2) + 1));
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

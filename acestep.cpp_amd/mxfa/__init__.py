@@ -22,7 +22,9 @@ from dataclasses import dataclass
 from typing import Optional
 
 _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(_PKG_DIR, "lib", "libmxfa.so")
+# MXFA_LIB names another build of the library (e.g. an instrumented one);
+# the default is the in-tree build.
+LIB_PATH = os.environ.get("MXFA_LIB") or os.path.join(_PKG_DIR, "lib", "libmxfa.so")
 
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_BF16 = 0, 1, 8, 30
 PREC_DEFAULT, PREC_F32 = 0, 10
