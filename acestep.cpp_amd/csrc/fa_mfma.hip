@@ -210,22 +210,6 @@ fa_prefill_kernel(const FaArgs a) {
     const bool row_ok = qrow < a.Sq;
     const int qrow_c = row_ok ? qrow : a.Sq - 1;
 
-    // Q^T operand for the 8 dim-steps of 16: Q[qrow][16t + 8h + e].
-    V8 qb[8];
-    {
-        const float *qp = (const float *)(a.q + (int64_t)qrow_c * a.q_nb1 + (int64_t)head * a.q_nb2 +
-                                          (int64_t)b * a.q_nb3);
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-            f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
-            if (row_ok) {
-                x0 = *(const f32x4 *)(qp + 16 * t + 8 * h);
-                x1 = *(const f32x4 *)(qp + 16 * t + 8 * h + 4);
-            }
-            qb[t] = __builtin_bit_cast(V8, cvt8<T>(x0, x1));
-        }
-    }
-
     const int plane = a.mask ? (b % a.m_ne3) * a.m_ne2 + head % a.m_ne2 : 0;
     TileClasses tc{0u, 0u, a.tile_class != nullptr};
     if (tc.present) {
@@ -292,6 +276,27 @@ fa_prefill_kernel(const FaArgs a) {
             dma16_buf(rv, vv[c], l0 + kTileBytes + 4 * c * 256);
         }
     };
+
+    // The first live tile's copies go out before Q is loaded: the two
+    // fetches share one memory latency.
+    int kt = tc.next_live(0, n_kt);
+    if (kt < n_kt) issue(kt, std::integral_constant<int, 0>{});
+
+    // Q^T operand for the 8 dim-steps of 16: Q[qrow][16t + 8h + e].
+    V8 qb[8];
+    {
+        const float *qp = (const float *)(a.q + (int64_t)qrow_c * a.q_nb1 + (int64_t)head * a.q_nb2 +
+                                          (int64_t)b * a.q_nb3);
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
+            if (row_ok) {
+                x0 = *(const f32x4 *)(qp + 16 * t + 8 * h);
+                x1 = *(const f32x4 *)(qp + 16 * t + 8 * h + 4);
+            }
+            qb[t] = __builtin_bit_cast(V8, cvt8<T>(x0, x1));
+        }
+    }
 
     // LDS operand addresses.  QK: K operand of dim-step t for key l32 of a
     // half: chunk (2t + h) ^ swz_k(l32) of row l32.  PV: V^T operand of dim
@@ -468,8 +473,6 @@ fa_prefill_kernel(const FaArgs a) {
     // anywhere: they would put the tile loop under divergent control flow.)
     std::integral_constant<int, 0> st0;
     std::integral_constant<int, 1> st1;
-    int kt = tc.next_live(0, n_kt);
-    if (kt < n_kt) issue(kt, st0);
     while (kt < n_kt) {
         int kn = tc.next_live(kt + 1, n_kt);
         MXFA_WAIT_VMCNT(0);

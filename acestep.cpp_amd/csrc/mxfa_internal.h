@@ -17,7 +17,7 @@ hipError_t launch_fa_decode(const FaArgs &a, int ktype, hipStream_t stream);
 hipError_t launch_fill_zero(int *p, int64_t n, hipStream_t stream);
 
 // MFMA prefill kernel geometry.
-constexpr int kPfBM = 128;   // query rows per workgroup (4 query blocks x 32, each served by two waves)
+constexpr int kPfBM = 128;   // query rows per workgroup (4 waves x 32)
 constexpr int kPfBN = 64;    // keys per K/V tile
 
 // Mask tile classifier: writes a.tile_class[plane][qt][kt] (row stride

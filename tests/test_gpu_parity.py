@@ -193,6 +193,12 @@ def _rand_case(seed, B=2, Bk=None, Sq=5, Nh=8, Nkv=2, Skv=300, kv_type=1, mask="
         elif mask == "causal":
             allowed = np.arange(Skv)[None, :] <= (Skv - Sq + np.arange(Sq))[:, None]
             vals = np.broadcast_to(np.where(allowed, 0.0, -np.inf), (B, Hm, Sq, Skv))
+        elif mask == "band":
+            # a sliding window (the DiT sliding mask) whose first 256 queries
+            # see every key: a few long query tiles among short ones
+            qi, kj = np.arange(Sq)[:, None], np.arange(Skv)[None, :]
+            allowed = (np.abs(qi - kj) <= 96) | (qi < 256)
+            vals = np.broadcast_to(np.where(allowed, 0.0, -np.inf), (B, Hm, Sq, Skv))
         vals = np.asarray(vals, dtype=np.float32)
         if max_bias > 0:
             vals = np.where(np.isneginf(vals), vals, -np.abs(vals) * 3).astype(np.float32)
@@ -300,6 +306,16 @@ def test_causal_prefill_offsets(mx):
     # prompt continuation: Sq new tokens at the end of a longer window
     c = _rand_case(80, B=1, Sq=300, Nh=8, Nkv=2, Skv=1000, mask="causal")
     check(mx, c, "causal continuation 300 of 1000")
+
+
+@pytest.mark.parametrize("mask", ["causal", "band"])
+def test_prefill_row_split(mx, mask):
+    # long query tiles among short ones: the prefill kernel shares the long
+    # rows between two workgroups and merges their partials (per-head mask
+    # planes for the band case, so the plane means differ)
+    heads = 1 if mask == "causal" else 2
+    c = _rand_case(90, B=2, Sq=1100, Nh=4, Nkv=2, Skv=1100, mask=mask, mask_heads=heads)
+    check(mx, c, f"row split ({mask})")
 
 
 def test_workspace_grows_and_repeats(mx):
