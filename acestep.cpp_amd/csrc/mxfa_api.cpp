@@ -5,7 +5,9 @@
 //   * split-KV decode kernel (fa_decode.hip) when few query rows share a
 //     KV head: decode (Sq = 1) and short prompts, and every Q8_0 K/V call;
 //   * MFMA prefill kernel (fa_mfma.hip) for long query runs (prefill, DiT),
-//     preceded by the mask tile classifier when a mask is given.
+//     preceded by the mask tile classifier when a mask is given;
+// and GGML_OP_SET_ROWS, the KV-cache write before each attention node
+// (set_rows.hip).
 // The only memory the engine owns is per device and grow-only: a workspace
 // (split partials, mask tile classes) and the split tickets, freed by
 // mxfa_release().  Calls that overlap on one device (different streams)
@@ -78,6 +80,77 @@ size_t type_block_bytes(int type) {
         case MXFA_TYPE_Q8_0: return 34;
         default: return 0;
     }
+}
+
+// Validation of a GGML_OP_SET_ROWS node (the shape asserts of ggml_set_rows
+// plus this kernel's layout needs).  Fills `a` when `a` is given.
+int check_set_rows(const mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_tensor *rows, SetRowsArgs *a) {
+    if (!dst || !src || !rows) return fail(MXFA_ERR_INVALID, "dst, src and rows are required");
+    for (const mxfa_tensor *t : {dst, src, rows})
+        for (int i = 0; i < 4; i++)
+            if (t->ne[i] < 0) return fail(MXFA_ERR_INVALID, "ne[%d] = %lld is negative", i, (long long)t->ne[i]);
+    if (src->type != MXFA_TYPE_F32) return fail(MXFA_ERR_UNSUPPORTED, "set_rows source must be F32 (type %d)", src->type);
+    if (rows->type != MXFA_TYPE_I64 && rows->type != MXFA_TYPE_I32)
+        return fail(MXFA_ERR_INVALID, "row ids must be I64 or I32 (type %d)", rows->type);
+    if (dst->ne[0] != src->ne[0] || dst->ne[2] != src->ne[2] || dst->ne[3] != src->ne[3])
+        return fail(MXFA_ERR_INVALID, "dst and src differ in ne[0], ne[2] or ne[3]");
+    if (src->ne[1] != rows->ne[0]) return fail(MXFA_ERR_INVALID, "src->ne[1] != rows->ne[0]");
+    if (rows->ne[1] < 1 || rows->ne[2] < 1 || rows->ne[3] != 1)
+        return fail(MXFA_ERR_INVALID, "rows must be [n, R1 >= 1, R2 >= 1, 1]");
+    if (src->ne[2] % rows->ne[1] || src->ne[3] % rows->ne[2])
+        return fail(MXFA_ERR_INVALID, "row ids do not broadcast over src->ne[2] / ne[3]");
+    const int dt = dst->type;
+    if (dt != MXFA_TYPE_F32 && dt != MXFA_TYPE_F16 && dt != MXFA_TYPE_BF16 && dt != MXFA_TYPE_Q8_0)
+        return fail(MXFA_ERR_UNSUPPORTED, "set_rows destination type %d (F32, F16, BF16, Q8_0)", dt);
+    const int64_t D = src->ne[0];
+    if (dt == MXFA_TYPE_Q8_0 ? D % 32 != 0 : D % 4 != 0)
+        return fail(MXFA_ERR_UNSUPPORTED, "row length %lld (needs a multiple of %d)", (long long)D,
+                    dt == MXFA_TYPE_Q8_0 ? 32 : 4);
+    if (src->nb[0] != 4 || dst->nb[0] != type_block_bytes(dt))
+        return fail(MXFA_ERR_UNSUPPORTED, "src/dst rows must be contiguous");
+    if (rows->nb[0] != (rows->type == MXFA_TYPE_I64 ? 8u : 4u))
+        return fail(MXFA_ERR_INVALID, "row ids must be contiguous along ne[0]");
+    const int64_t n_rows = src->ne[1] * src->ne[2] * src->ne[3];
+    if (n_rows == 0 || D == 0) {
+        if (a) *a = SetRowsArgs{};
+        return MXFA_OK;   // empty source: nothing to write
+    }
+    if (!dst->data || !src->data || !rows->data) return fail(MXFA_ERR_INVALID, "NULL data pointer");
+    if (!is_aligned(src->data, 16) || src->nb[1] % 16 || src->nb[2] % 16 || src->nb[3] % 16)
+        return fail(MXFA_ERR_UNSUPPORTED, "src data/strides must be 16-byte aligned");
+    const size_t da = dt == MXFA_TYPE_F32 ? 16 : dt == MXFA_TYPE_Q8_0 ? 2 : 8;
+    if (!is_aligned(dst->data, da) || dst->nb[1] % da || dst->nb[2] % da || dst->nb[3] % da)
+        return fail(MXFA_ERR_UNSUPPORTED, "dst data/strides must be %zu-byte aligned", da);
+    const size_t ia = rows->nb[0];
+    if (!is_aligned(rows->data, ia) || rows->nb[1] % ia || rows->nb[2] % ia)
+        return fail(MXFA_ERR_INVALID, "row ids misaligned");
+    if (n_rows * (D / 4) >= ((int64_t)1 << 31))
+        return fail(MXFA_ERR_UNSUPPORTED, "set_rows source too large for one launch");
+    if (a) {
+        SetRowsArgs &r = *a;
+        r = SetRowsArgs{};
+        r.src = (const char *)src->data;
+        r.rows = (const char *)rows->data;
+        r.dst = (char *)dst->data;
+        r.cpr = (uint32_t)(D / 4);
+        r.ne01 = (uint32_t)src->ne[1];
+        r.ne02 = (uint32_t)src->ne[2];
+        r.n_rows = (uint32_t)n_rows;
+        r.r_ne1 = (uint32_t)rows->ne[1];
+        r.r_ne2 = (uint32_t)rows->ne[2];
+        r.s_nb1 = (int64_t)src->nb[1];
+        r.s_nb2 = (int64_t)src->nb[2];
+        r.s_nb3 = (int64_t)src->nb[3];
+        r.r_nb0 = (int64_t)rows->nb[0];
+        r.r_nb1 = (int64_t)rows->nb[1];
+        r.r_nb2 = (int64_t)rows->nb[2];
+        r.d_nb1 = (int64_t)dst->nb[1];
+        r.d_nb2 = (int64_t)dst->nb[2];
+        r.d_nb3 = (int64_t)dst->nb[3];
+        r.dst_ne1 = dst->ne[1];
+        r.rows_i64 = rows->type == MXFA_TYPE_I64;
+    }
+    return MXFA_OK;
 }
 
 struct Plan {
@@ -415,6 +488,21 @@ int mxfa_flash_attn_ext(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_t
     }
     e = launch_fa_decode(a, pl.ktype, stream);
     if (e != hipSuccess) return fail(MXFA_ERR_HIP, "decode launch: %s", hipGetErrorString(e));
+    return MXFA_OK;
+}
+
+int mxfa_set_rows_supports(const mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_tensor *rows) {
+    return check_set_rows(dst, src, rows, nullptr) == MXFA_OK ? 1 : 0;
+}
+
+int mxfa_set_rows(mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_tensor *rows, void *hip_stream) {
+    SetRowsArgs a;
+    const int rc = check_set_rows(dst, src, rows, &a);
+    if (rc != MXFA_OK) return rc;
+    if (a.n_rows == 0) return MXFA_OK;
+    hipStream_t stream = (hipStream_t)hip_stream;
+    const hipError_t e = timed_launch("set_rows", stream, [&] { return launch_set_rows(a, dst->type, stream); });
+    if (e != hipSuccess) return fail(MXFA_ERR_HIP, "set_rows launch: %s", hipGetErrorString(e));
     return MXFA_OK;
 }
 

@@ -29,6 +29,27 @@ hipError_t launch_mask_classify(const FaArgs &a, int n_planes, uint8_t *classes,
 // MFMA prefill / DiT kernel.  ktype: T_F16/T_BF16.
 hipError_t launch_fa_prefill(const FaArgs &a, int ktype, hipStream_t stream);
 
+// KV-cache write (GGML_OP_SET_ROWS, F32 source).  Source row r of the
+// flattened [ne01, ne02, ne03] row space goes to destination row
+// rows[r % ne01, i02 % r_ne1, i03 % r_ne2] of plane (i02, i03).
+struct SetRowsArgs {
+    const char *src;            // F32 rows
+    const char *rows;           // I64 (rows_i64) or I32 row ids
+    char *dst;                  // destination rows (dst_ne1 per plane)
+    uint32_t cpr;               // 4-value chunks per row (ne0 / 4)
+    uint32_t ne01, ne02, n_rows;                // n_rows = ne01*ne02*ne03 (< 2^31 chunks total)
+    uint32_t r_ne1, r_ne2;                      // row-id broadcast extents
+    int64_t s_nb1, s_nb2, s_nb3;                // source strides (bytes)
+    int64_t r_nb0, r_nb1, r_nb2;                // row-id strides
+    int64_t d_nb1, d_nb2, d_nb3, dst_ne1;       // destination strides, rows per plane
+    int rows_i64;
+};
+
+// ne0 % 4 == 0 (F32/F16/BF16) or ne0 % 32 == 0 (Q8_0); source rows 16-byte
+// aligned, F16/BF16 destination rows 8-byte aligned, F32 16-byte, Q8_0 2-byte;
+// n_rows * cpr < 2^31.
+hipError_t launch_set_rows(const SetRowsArgs &a, int dtype, hipStream_t stream);
+
 // Per-kernel timing: when enabled, timed_launch() brackets `launch` with
 // two events on `stream` and files them under `family`.
 bool timing_enabled();

@@ -6,7 +6,9 @@ It mirrors the reference's operator interface for this path:
 ggml_flash_attn_ext + ggml_flash_attn_ext_set_prec as acestep.cpp calls them
 (src/qwen3-lm.h:465-469, :789-794; src/dit-graph.h:227-231, :348-352;
 src/qwen3-enc.h:195-199), and ``supports`` is the backend's supports_op for
-GGML_OP_FLASH_ATTN_EXT.  Tensors are ggml views: a type id, ne[4], nb[4] and
+GGML_OP_FLASH_ATTN_EXT; ``set_rows`` / ``set_rows_supports`` do the same for
+the KV-cache write before it (ggml_set_rows, src/qwen3-lm.h:453-454,
+:776-777).  Tensors are ggml views: a type id, ne[4], nb[4] and
 a device pointer (`DeviceView`).  Device memory and streams come from torch
 (plumbing only); all arithmetic runs in the HIP kernels of libmxfa.so.
 
@@ -27,6 +29,7 @@ _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.environ.get("MXFA_LIB") or os.path.join(_PKG_DIR, "lib", "libmxfa.so")
 
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_BF16 = 0, 1, 8, 30
+TYPE_I32, TYPE_I64 = 26, 27
 PREC_DEFAULT, PREC_F32 = 0, 10
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NOMEM = 0, -1, -2, -3, -4
@@ -35,6 +38,8 @@ OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NOMEM = 0, -1, -2, -3, -4
 EXPORTED_SYMBOLS = (
     "mxfa_supports",
     "mxfa_flash_attn_ext",
+    "mxfa_set_rows_supports",
+    "mxfa_set_rows",
     "mxfa_release",
     "mxfa_status_string",
     "mxfa_last_error",
@@ -79,6 +84,10 @@ def _load():
     L.mxfa_supports.restype = ctypes.c_int
     L.mxfa_flash_attn_ext.argtypes = [P, P, P, P, ctypes.POINTER(MxfaParams), P, ctypes.c_void_p]
     L.mxfa_flash_attn_ext.restype = ctypes.c_int
+    L.mxfa_set_rows_supports.argtypes = [P, P, P]
+    L.mxfa_set_rows_supports.restype = ctypes.c_int
+    L.mxfa_set_rows.argtypes = [P, P, P, ctypes.c_void_p]
+    L.mxfa_set_rows.restype = ctypes.c_int
     L.mxfa_release.argtypes = []
     L.mxfa_release.restype = None
     L.mxfa_status_string.argtypes = [ctypes.c_int]
@@ -173,6 +182,30 @@ def flash_attn_ext(q, k, v, mask, scale, max_bias=0.0, logit_softcap=0.0, prec=P
     p = make_params(scale, max_bias, logit_softcap, prec)
     rc = lib.mxfa_flash_attn_ext(refs[0], refs[1], refs[2], refs[3], ctypes.byref(p), refs[4],
                                  ctypes.c_void_p(int(stream)))
+    if rc != OK:
+        raise MxfaError(rc, last_error())
+    return dst
+
+
+def set_rows_supports(dst, src, rows) -> bool:
+    """supports_op for GGML_OP_SET_ROWS (node = dst view, src[0] = src,
+    src[1] = rows)."""
+    dd, ds, dr = dst.desc(), src.desc(), rows.desc()
+    return bool(lib.mxfa_set_rows_supports(ctypes.byref(dd), ctypes.byref(ds), ctypes.byref(dr)))
+
+
+def set_rows(dst: DeviceView, src: DeviceView, rows: DeviceView, stream: Optional[int] = None) -> DeviceView:
+    """GGML_OP_SET_ROWS on the GPU, as ggml_set_rows(ctx, dst, src, rows) in
+    the reference's KV-cache write (src/qwen3-lm.h:453-454, :776-777): the F32
+    rows of `src` are converted to dst's type and written, in place, to the
+    rows of `dst` that `rows` (I64 / I32) names.  Asynchronous on `stream`
+    (default: torch's current stream).  Returns `dst`; raises MxfaError."""
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    dd, ds, dr = dst.desc(), src.desc(), rows.desc()
+    rc = lib.mxfa_set_rows(ctypes.byref(dd), ctypes.byref(ds), ctypes.byref(dr), ctypes.c_void_p(int(stream)))
     if rc != OK:
         raise MxfaError(rc, last_error())
     return dst

@@ -39,7 +39,8 @@ from . import synth
 
 TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_BF16 = 0, 1, 8, 30
 D = 128
-SEEDS = {"c1": 1001, "c2": 1002, "c3": 1003, "c4s": 1004, "c4x": 1005, "c5": 1006}
+SEEDS = {"c1": 1001, "c2": 1002, "c3": 1003, "c4s": 1004, "c4x": 1005, "c5": 1006,
+         "kw2": 1102, "kw3": 1103, "kw5": 1105}
 
 
 @dataclass
@@ -300,6 +301,101 @@ def c5(**kw) -> FaCase:
 
 
 BUILDERS = {"c1": c1, "c2": c2, "c3": c3, "c4s": c4_self, "c4x": c4_cross, "c5": c5}
+
+
+# -- KV-cache write (GGML_OP_SET_ROWS) -------------------------------------------
+
+TYPE_I32, TYPE_I64 = 26, 27
+
+
+@dataclass
+class SetRowsCase:
+    name: str
+    dst: HostView          # the cache view set_rows writes into
+    src: HostView          # F32 rows
+    rows: HostView         # I64 / I32 row ids
+    meta: dict = field(default_factory=dict)
+
+
+def _cache_fill(seed, n_bytes):
+    """Random bytes standing for whatever the cache held before the write
+    (rows the write does not name must keep them)."""
+    return synth.uniform_u32(seed, synth.STREAM_PAD, 0, -(-n_bytes // 4)).view(np.uint8)[:n_bytes].copy()
+
+
+def kv_write_single(name="kw2", seed=None, n_tokens=2048, kv_pos=0, Nkv=8, max_seq=2048,
+                    cache_type=TYPE_F16, row_type=TYPE_I64) -> SetRowsCase:
+    """qw3lm_build_attn's cache write (src/qwen3-lm.h:448-454): the
+    contiguous F32 [D, S, Nkv] rows (ggml_cont of the permuted RoPE output,
+    :433-436) go to rows kv_pos .. kv_pos+S-1 of the [D, max_seq, Nkv] cache;
+    kv_rows is I64 [S] (:528-530), broadcast over Nkv."""
+    seed = SEEDS.get(name, 1100) if seed is None else seed
+    S = n_tokens
+    assert kv_pos + S <= max_seq
+    src = HostView(TYPE_F32, (D, S, Nkv, 1), _contig_nb((D, S, Nkv, 1), 4),
+                   synth.normal(seed, synth.STREAM_K, 0, D * S * Nkv))
+    idt = np.int64 if row_type == TYPE_I64 else np.int32
+    rows = np.arange(kv_pos, kv_pos + S, dtype=idt)
+    rv = HostView(row_type, (S, 1, 1, 1), _contig_nb((S, 1, 1, 1), rows.itemsize), rows)
+    rb = _type_row_bytes(cache_type, D)
+    dnb = (_type_row_bytes(cache_type, 1) if cache_type != TYPE_Q8_0 else 34, rb, rb * max_seq, rb * max_seq * Nkv)
+    dst = HostView(cache_type, (D, max_seq, Nkv, 1), dnb, _cache_fill(seed, rb * max_seq * Nkv))
+    return SetRowsCase(name, dst, src, rv, meta=dict(seed=seed, S=S, kv_pos=kv_pos, Nkv=Nkv, max_seq=max_seq,
+                                                     kind="kv_write_single"))
+
+
+def kv_write_batch(name="kw3", seed=None, N=8, Nkv=8, max_seq=8192, n_sets=None, s0=0, positions=None,
+                   cache_type=TYPE_F16) -> SetRowsCase:
+    """qw3lm_forward_batch's cache write (src/qwen3-lm.h:760-777): one new
+    token per sequence; dst is the 4D view [D, max_seq, Nkv, N] of the
+    [D, max_seq, Nkv, n_sets] cache starting at set s0, src the F32
+    [D, 1, Nkv, N] rows, kv_rows I64 [1, 1, N] one position per set
+    (:699-701), broadcast over Nkv."""
+    seed = SEEDS.get(name, 1101) if seed is None else seed
+    n_sets = N + s0 if n_sets is None else n_sets
+    assert s0 + N <= n_sets
+    if positions is None:
+        positions = synth.uniform_int(seed, synth.STREAM_LEN, 0, N, 0, max_seq - 1)
+    positions = np.asarray(positions, dtype=np.int64)
+    src = HostView(TYPE_F32, (D, 1, Nkv, N), _contig_nb((D, 1, Nkv, N), 4),
+                   synth.normal(seed, synth.STREAM_K, 0, D * Nkv * N))
+    rv = HostView(TYPE_I64, (1, 1, N, 1), (8, 8, 8, 8 * N), positions.copy())
+    rb = _type_row_bytes(cache_type, D)
+    nb = (_type_row_bytes(cache_type, 1) if cache_type != TYPE_Q8_0 else 34, rb, rb * max_seq, rb * max_seq * Nkv)
+    buf = _cache_fill(seed, nb[3] * n_sets)
+    dst = HostView(cache_type, (D, max_seq, Nkv, N), nb, buf, offset=s0 * nb[3])
+    return SetRowsCase(name, dst, src, rv, meta=dict(seed=seed, N=N, Nkv=Nkv, max_seq=max_seq, s0=s0,
+                                                     positions=positions.tolist(), kind="kv_write_batch"))
+
+
+def kw2(**kw) -> SetRowsCase:
+    """C2's cache write: 2048 prompt tokens x 8 KV heads into the F16 cache."""
+    return kv_write_single("kw2", **kw)
+
+
+def kw3(**kw) -> SetRowsCase:
+    """C3's cache write: one token for each of 8 sequences, 8 KV heads."""
+    return kv_write_batch("kw3", **kw)
+
+
+def kw5(**kw) -> SetRowsCase:
+    """C2's cache write into a Q8_0 cache (quantised on the fly)."""
+    kw.setdefault("cache_type", TYPE_Q8_0)
+    return kv_write_single("kw5", **kw)
+
+
+SET_ROWS_BUILDERS = {"kw2": kw2, "kw3": kw3, "kw5": kw5}
+
+
+def set_rows_work(case: SetRowsCase) -> dict:
+    """Algorithmic bytes of one set_rows call: every F32 source row read once,
+    its converted row written once, the row ids read once."""
+    n = int(case.src.ne[1] * case.src.ne[2] * case.src.ne[3])
+    r = case.rows
+    rd = n * 4 * D
+    wr = n * _type_row_bytes(case.dst.type, D)
+    ids = int(r.ne[0] * r.ne[1] * r.ne[2]) * (8 if r.type == TYPE_I64 else 4)
+    return dict(rows=n, read_bytes=rd, write_bytes=wr, id_bytes=ids, bytes=rd + wr + ids)
 
 
 # -- work accounting -----------------------------------------------------------

@@ -18,7 +18,9 @@ heads, D=128, F32 Q, F16 K/V in a 2048-slot cache, F16 causal mask.  One
 
 The other configurations (C1, C3, C4 self/cross, C5) are reported under
 "configs" with their own bound (TFLOP/s vs MFMA peak, or KV GB/s vs the 8 TB/s
-HBM peak).  Inputs of bandwidth-bound configs are rotated over enough device
+HBM peak), and so are the KV-cache writes that precede C2 / C3 (GGML_OP_SET_ROWS:
+kw2, kw3, and kw5 into a Q8_0 cache; GB/s of F32 read + converted row
+written + row ids, vs the HBM peak).  Inputs of bandwidth-bound configs are rotated over enough device
 copies that consecutive steps do not hit in the 256 MB Infinity Cache.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2,c3] [--no-cpu]
@@ -53,6 +55,11 @@ DESCR = {
     "c4x": "DiT cross-attention: B=2, 3000 q x 256 keys, 16/16 heads, D=128, F16 KV, padding mask 0-128",
     "c5": "Qwen3-4B decode over Q8_0 KV: B=4, 32/8 heads, D=128, KV 8192",
 }
+DESCR.update({
+    "kw2": "KV-cache write (GGML_OP_SET_ROWS) of C2: 2048 tokens x 8 KV heads, F32 -> F16 cache [128, 2048, 8]",
+    "kw3": "KV-cache write of C3: 1 token x 8 KV heads for each of 8 sets, F32 -> F16 4D cache view",
+    "kw5": "KV-cache write of C2 into a Q8_0 cache: 2048 tokens x 8 KV heads, F32 -> Q8_0",
+})
 BOUND = {"c1": "hbm", "c2": "mfma", "c3": "hbm", "c4s": "mfma", "c4x": "hbm", "c5": "hbm"}
 KERNEL = {"c1": "fa_decode", "c2": "fa_prefill", "c3": "fa_decode", "c4s": "fa_prefill", "c4x": "fa_prefill",
           "c5": "fa_decode"}
@@ -118,6 +125,55 @@ def time_case(mx, torch, case, steps, warmup, rotate_bytes=None):
     del copies, outs
     torch.cuda.empty_cache()
     return ms, kern, w, n_copies
+
+
+def time_set_rows(mx, torch, case, steps, warmup, rotate_bytes=ROTATE_BYTES):
+    """set_rows timing: (ms per call, kernel avg ms, work, copies).  Source
+    and cache are rotated over enough copies to exceed the Infinity Cache."""
+    from mxfa import cases as C
+
+    w = C.set_rows_work(case)
+    n_copies = int(min(64, max(1, math.ceil(rotate_bytes / max(w["bytes"], 1)))))
+    copies = [(mx.upload(case.dst), mx.upload(case.src), mx.upload(case.rows)) for _ in range(n_copies)]
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step(i):
+        d, s, r = copies[i % n_copies]
+        mx.set_rows(d, s, r, stream=stream)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(steps):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    mx.timing_reset()
+    mx.timing_enable(True)
+    for i in range(steps):
+        step(i)
+    torch.cuda.synchronize()
+    mx.timing_enable(False)
+    tot, n = mx.timing_read("set_rows")
+    mx.timing_reset()
+    del copies
+    torch.cuda.empty_cache()
+    return ms, (tot / n if n else None), w, n_copies
+
+
+def summarize_set_rows(name, ms, kms, w, n_copies):
+    out = dict(workload=DESCR[name], ms=round(ms, 5), bytes=w["bytes"], rows=w["rows"], copies=n_copies,
+               bound="hbm")
+    out["gbs"] = round(w["bytes"] / (ms * 1e-3) / 1e9, 2)
+    out["frac_peak"] = round(out["gbs"] / PEAK_GBS, 4)
+    if kms:
+        out["kernel_ms"] = round(kms, 5)
+        out["kernel_gbs"] = round(w["bytes"] / (kms * 1e-3) / 1e9, 2)
+        out["kernel_frac_peak"] = round(out["kernel_gbs"] / PEAK_GBS, 4)
+    return out
 
 
 def summarize(name, ms, kern, w, n_copies):
@@ -206,7 +262,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5")
+    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,kw2,kw3,kw5")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB copy (counter calibration under rocprofv3)")
@@ -234,6 +290,12 @@ def main():
     headline = None
     for name in names:
         log(f"[bench] building {name} ...")
+        if name in C.SET_ROWS_BUILDERS:
+            case = C.SET_ROWS_BUILDERS[name]()
+            ms, kms, w, ncp = time_set_rows(mxfa, torch, case, args.steps, args.warmup)
+            results[name] = summarize_set_rows(name, ms, kms, w, ncp)
+            log(f"[bench] {name}: {json.dumps(results[name])}")
+            continue
         case = C.BUILDERS[name]()
         # supports_op reads descriptors only: a placeholder aligned address will do
         fake = lambda t: mxfa.DeviceView(t.type, tuple(t.ne), tuple(t.nb), 1 << 20)  # noqa: E731

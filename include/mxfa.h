@@ -49,6 +49,8 @@ extern "C" {
 #define MXFA_TYPE_F16  1
 #define MXFA_TYPE_Q8_0 8
 #define MXFA_TYPE_BF16 30
+#define MXFA_TYPE_I32  26   /* set_rows row ids */
+#define MXFA_TYPE_I64  27
 
 /* ggml_prec values (GGML_PREC_DEFAULT / GGML_PREC_F32).  The engine always
  * accumulates in fp32, so both are accepted and treated alike. */
@@ -99,6 +101,33 @@ int mxfa_flash_attn_ext(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_t
                         const mxfa_tensor *mask, const mxfa_params *params, mxfa_tensor *dst,
                         void *hip_stream);
 
+/* GGML_OP_SET_ROWS with an F32 source: the KV-cache write the reference
+ * issues right before each attention node, ggml_set_rows(ctx, cache, rows_f32,
+ * kv_rows) at src/qwen3-lm.h:453-454 ([D, S, Nkv] rows into the
+ * [D, max_seq, Nkv] F16 cache, row ids [S] broadcast over Nkv) and :776-777
+ * ([D, 1, Nkv, N] rows into N cache sets, row ids [1, 1, N]).  A ggml
+ * backend maps the node as (dst = node, src = node->src[0],
+ * rows = node->src[1]):
+ *
+ *   src  : F32             [D, n, ne2, ne3], nb[0] = 4
+ *   rows : I64 | I32       [n, R1, R2, 1] with ne2 % R1 == 0, ne3 % R2 == 0
+ *   dst  : F32|F16|BF16|Q8_0 [D, M, ne2, ne3] (the cache view)
+ *
+ *   dst[:, rows[i, i2 % R1, i3 % R2], i2, i3] = convert(src[:, i, i2, i3])
+ *
+ * convert = ggml's from_float of dst's type: F16 / BF16 round to nearest
+ * even, Q8_0 per 32 values d = amax/127 (stored F16), q = round-half-even(
+ * x * 127/amax).  Row ids live in device memory and are not read on the
+ * host: a row whose id is outside [0, M) is skipped (ggml's CPU backend
+ * aborts on it).  Rows that name the same destination row race (ggml leaves
+ * that order unspecified too).  Needs D % 4 == 0 (D % 32 for Q8_0), src data
+ * and strides 16-byte aligned, dst rows contiguous.  Launches one kernel on
+ * `hip_stream`, allocates nothing, returns MXFA_OK or a negative status
+ * (nothing launched on failure).  An empty source (n, ne2 or ne3 = 0) is a
+ * no-op. */
+int mxfa_set_rows_supports(const mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_tensor *rows);
+int mxfa_set_rows(mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_tensor *rows, void *hip_stream);
+
 /* Free the workspaces of every device (synchronises each device first). */
 void mxfa_release(void);
 
@@ -114,7 +143,7 @@ int mxfa_version(void);
  * enabled, every kernel the engine launches is bracketed by two HIP events
  * recorded on its launch stream.  mxfa_timing_read() waits for the recorded
  * events, returns the summed duration (ms) and launch count of one kernel
- * family ("fa_prefill", "mask_classify", "fa_decode") since the
+ * family ("fa_prefill", "mask_classify", "fa_decode", "set_rows") since the
  * last reset, and mxfa_timing_reset() clears all counters.  Disabled by
  * default; enabling it adds two event records per launch. */
 void mxfa_timing_enable(int on);

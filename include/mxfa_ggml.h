@@ -1,6 +1,6 @@
 /*
- * mxfa_ggml.h -- header-only adapter from a ggml GGML_OP_FLASH_ATTN_EXT node
- * to the mxfa C ABI (include/mxfa.h).
+ * mxfa_ggml.h -- header-only adapter from ggml GGML_OP_FLASH_ATTN_EXT and
+ * GGML_OP_SET_ROWS nodes to the mxfa C ABI (include/mxfa.h).
  *
  * Include it after ggml.h in a ggml backend.  The backend's supports_op and
  * graph_compute, on a node it has already identified as
@@ -9,6 +9,11 @@
  *
  *     mxfa_ggml_supports(node)                 -> 1 / 0
  *     mxfa_ggml_flash_attn_ext(node, stream)   -> MXFA_OK / negative status
+ *
+ * and on a GGML_OP_SET_ROWS node (the KV-cache write before attention)
+ *
+ *     mxfa_ggml_set_rows_supports(node)        -> 1 / 0
+ *     mxfa_ggml_set_rows(node, stream)         -> MXFA_OK / negative status
  *
  * The node layout is the one ggml_flash_attn_ext builds (upstream ggml; the
  * reference's call sites are src/qwen3-lm.h:465-469, :789-794,
@@ -83,6 +88,24 @@ static inline int mxfa_ggml_supports(const struct ggml_tensor *node) {
     if (!node || !node->src[0] || !node->src[1] || !node->src[2]) return 0;
     if (mxfa_ggml_unpack(node, &q, &k, &v, &m, &mp, &d, &p) != 0) return 0;
     return mxfa_supports(&q, &k, &v, mp, &p, &d);
+}
+
+/* supports_op / graph_compute for a GGML_OP_SET_ROWS node, the KV-cache
+ * write (ggml_set_rows(ctx, a, b, c) at src/qwen3-lm.h:453-454, :776-777):
+ * the node is a view of the destination `a`, node->src[0] = b (F32 rows),
+ * node->src[1] = c (I64 / I32 row ids). */
+static inline int mxfa_ggml_set_rows_supports(const struct ggml_tensor *node) {
+    mxfa_tensor d, s, r;
+    if (!node || !node->src[0] || !node->src[1]) return 0;
+    return mxfa_set_rows_supports(mxfa_ggml_desc(node, &d), mxfa_ggml_desc(node->src[0], &s),
+                                  mxfa_ggml_desc(node->src[1], &r));
+}
+
+static inline int mxfa_ggml_set_rows(const struct ggml_tensor *node, void *hip_stream) {
+    mxfa_tensor d, s, r;
+    if (!node || !node->src[0] || !node->src[1]) return MXFA_ERR_INVALID;
+    mxfa_ggml_desc(node, &d);
+    return mxfa_set_rows(&d, mxfa_ggml_desc(node->src[0], &s), mxfa_ggml_desc(node->src[1], &r), hip_stream);
 }
 
 /* graph_compute for a GGML_OP_FLASH_ATTN_EXT node on `hip_stream`. */

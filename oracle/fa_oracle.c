@@ -1,5 +1,6 @@
 /*
- * fa_oracle.c -- CPU oracle for GGML_OP_FLASH_ATTN_EXT.
+ * fa_oracle.c -- CPU oracle for GGML_OP_FLASH_ATTN_EXT and for the KV-cache
+ * write before it, GGML_OP_SET_ROWS (ora_set_rows, at the end of this file).
  *
  * TEST INFRASTRUCTURE ONLY.  This file is the checker, never the product:
  * only tests/, __graft_entry__.smoke() and the cpu_baseline leg of bench.py
@@ -625,4 +626,58 @@ int ora_fa_exact(const ora_tensor *q, const ora_tensor *k, const ora_tensor *v, 
     for (int t = 1; t < n_threads; t++) pthread_join(th[t], NULL);
     free(jobs); free(th);
     return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* GGML_OP_SET_ROWS (the KV-cache write), restated from ggml's published CPU  */
+/* kernel (ggml-cpu ops.cpp, ggml_compute_forward_set_rows_f32, upstream      */
+/* ggml late 2025; the ggml submodule is empty in the reference checkout).   */
+/* The reference calls it at src/qwen3-lm.h:453-454 (F32 [D, S, Nkv] rows    */
+/* into the F16 [D, max_seq, Nkv] cache, row ids [S] broadcast over Nkv) and  */
+/* :776-777 ([D, 1, Nkv, N] rows into N cache sets, row ids [1, 1, N]).       */
+/*                                                                            */
+/*   for i03 < ne03, i02 < ne02, i < ne01:                                    */
+/*     i1 = rows[i, i02 % rows.ne1, i03 % rows.ne2]   (I64 or I32)            */
+/*     dst[:, i1, i02, i03] = from_float(src[:, i, i02, i03])                 */
+/*                                                                            */
+/* from_float: F32 copy, F16 / BF16 with the codecs above, Q8_0 with          */
+/* ora_quantize_q8_0.  ggml asserts 0 <= i1 < dst.ne1; here such a row is     */
+/* skipped and counted (the GPU kernel skips it too).                         */
+/* Returns the number of skipped rows, or -1 when the shapes do not form a    */
+/* set_rows node.                                                             */
+/* ------------------------------------------------------------------------ */
+int64_t ora_set_rows(const ora_tensor *dst, const ora_tensor *src, const ora_tensor *rows) {
+    const int64_t D = src->ne[0];
+    if (src->type != ORA_F32 || (rows->type != 26 && rows->type != 27)) return -1;
+    if (dst->ne[0] != D || dst->ne[2] != src->ne[2] || dst->ne[3] != src->ne[3]) return -1;
+    if (src->ne[1] != rows->ne[0] || rows->ne[1] < 1 || rows->ne[2] < 1 || rows->ne[3] != 1) return -1;
+    if (src->ne[2] % rows->ne[1] || src->ne[3] % rows->ne[2]) return -1;
+    if (dst->type == ORA_Q8_0 && D % QK8_0) return -1;
+    if (dst->type != ORA_F32 && dst->type != ORA_F16 && dst->type != ORA_BF16 && dst->type != ORA_Q8_0)
+        return -1;
+    int64_t skipped = 0;
+    for (int64_t i03 = 0; i03 < src->ne[3]; i03++)
+        for (int64_t i02 = 0; i02 < src->ne[2]; i02++)
+            for (int64_t i = 0; i < src->ne[1]; i++) {
+                const char *ip = (const char *)rows->data + i * rows->nb[0] +
+                                 (i02 % rows->ne[1]) * rows->nb[1] + (i03 % rows->ne[2]) * rows->nb[2];
+                int64_t i1;
+                if (rows->type == 27) memcpy(&i1, ip, 8);
+                else { int32_t t; memcpy(&t, ip, 4); i1 = t; }
+                if (i1 < 0 || i1 >= dst->ne[1]) { skipped++; continue; }
+                const float *x = (const float *)((const char *)src->data + i * src->nb[1] +
+                                                 i02 * src->nb[2] + i03 * src->nb[3]);
+                char *y = (char *)dst->data + i1 * dst->nb[1] + i02 * dst->nb[2] + i03 * dst->nb[3];
+                switch (dst->type) {
+                    case ORA_F32: memcpy(y, x, (size_t)D * 4); break;
+                    case ORA_F16:
+                        for (int64_t j = 0; j < D; j++) { uint16_t h = ora_f2h(x[j]); memcpy(y + 2 * j, &h, 2); }
+                        break;
+                    case ORA_BF16:
+                        for (int64_t j = 0; j < D; j++) { uint16_t h = ora_f2bf(x[j]); memcpy(y + 2 * j, &h, 2); }
+                        break;
+                    default: ora_quantize_q8_0(x, (uint8_t *)y, D); break;
+                }
+            }
+    return skipped;
 }

@@ -11,6 +11,8 @@ fa_ggml(q, k, v, mask, scale, ..., acc_f32=False) -> float32 [B, Sq, Nh, DV]
     acc_f32=True runs the same algorithm with an fp32 V accumulator.
 fa_exact(q, k, v, mask, scale, ...) -> float64 [B, Sq, Nh, DV]
     fp64 two-pass softmax reference of the same op.
+set_rows(dst, src, rows) -> skipped rows
+    restatement of ggml's CPU set_rows (the KV-cache write), in place on dst.
 
 Inputs are `HostTensor`s: raw host bytes plus ggml type / ne / nb, so the
 oracle reads exactly the strided views the reference builds.
@@ -26,7 +28,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "build", "libfa_oracle.so")
 
-F32, F16, Q8_0, BF16 = 0, 1, 8, 30
+F32, F16, Q8_0, BF16, I32, I64 = 0, 1, 8, 30, 26, 27
 
 
 class _OraTensor(ctypes.Structure):
@@ -88,6 +90,8 @@ def lib():
             getattr(L, name).argtypes = [ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
             getattr(L, name).restype = ctypes.c_float
         L.ora_mad_f16.argtypes = [ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float]
+        L.ora_set_rows.argtypes = [P, P, P]
+        L.ora_set_rows.restype = ctypes.c_int64
         L.ora_set_force_scalar.argtypes = [ctypes.c_int]
         L.ora_simd_available.restype = ctypes.c_int
         _lib = L
@@ -188,3 +192,16 @@ def dequantize_q8_0(y: np.ndarray, n: int) -> np.ndarray:
     x = np.empty(n, dtype=np.float32)
     lib().ora_dequantize_q8_0(y.ctypes.data, x.ctypes.data, n)
     return x
+
+
+# -- KV-cache write (GGML_OP_SET_ROWS) -----------------------------------------
+
+def set_rows(dst: HostTensor, src: HostTensor, rows: HostTensor) -> int:
+    """ggml set_rows on host views: converts src's F32 rows into dst (in
+    place) at the rows that `rows` names; returns the number of rows skipped
+    for an out-of-range id."""
+    dd, ds, dr = _desc(dst), _desc(src), _desc(rows)
+    n = lib().ora_set_rows(ctypes.byref(dd), ctypes.byref(ds), ctypes.byref(dr))
+    if n < 0:
+        raise ValueError("ora_set_rows rejected the shapes")
+    return int(n)

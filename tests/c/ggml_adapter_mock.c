@@ -1,6 +1,7 @@
 /* Compiles include/mxfa_ggml.h against a mock struct ggml_tensor (the
  * fields the adapter reads, in ggml's order) and prints the descriptors it
- * derives from a flash-attention node, plus mxfa_supports()'s verdict.
+ * derives from a flash-attention node, plus mxfa_supports()'s verdict, and
+ * the set_rows adapter's verdicts on a KV-cache write node.
  * Built and run by tests/test_ggml_adapter.py. */
 #include <stdint.h>
 #include <stdio.h>
@@ -72,5 +73,19 @@ int main(int argc, char **argv) {
         printf("params scale=%.9g max_bias=%g softcap=%g prec=%d\n", p.scale, p.max_bias, p.logit_softcap, p.prec);
     }
     printf("supports %d\n", mxfa_ggml_supports(&node));
+
+    /* the KV-cache write before it (src/qwen3-lm.h:760-777): node = view of
+     * the [128, 8192, 8, 8] F16 cache sets, src[0] = F32 [128, 1, 8, 8] rows,
+     * src[1] = I64 [1, 1, 8] positions */
+    struct ggml_tensor sr, kn, ids;
+    memset(&sr, 0, sizeof sr); memset(&kn, 0, sizeof kn); memset(&ids, 0, sizeof ids);
+    sr = k; sr.src[0] = &kn; sr.src[1] = &ids;
+    kn.type = 0; set4(kn.ne, 128, 1, 8, 8); contig(&kn, 4); kn.data = (void *)(uintptr_t)0x600000;
+    ids.type = 27; set4(ids.ne, 1, 1, 8, 1); contig(&ids, 8); ids.data = (void *)(uintptr_t)0x700000;
+    printf("set_rows_supports %d\n", mxfa_ggml_set_rows_supports(&sr));
+    ids.type = 28;   /* F64: not a row-id type */
+    printf("set_rows_bad_ids %d\n", mxfa_ggml_set_rows_supports(&sr));
+    sr.src[1] = NULL;
+    printf("set_rows_no_ids %d %d\n", mxfa_ggml_set_rows_supports(&sr), mxfa_ggml_set_rows(&sr, NULL));
     return 0;
 }

@@ -50,3 +50,12 @@ def test_null_mask_and_sinks(exe):
     assert o["mask"] == "NULL" and o["supports"] == "1"
     o = run(exe, "sinks")
     assert o["unpack"] == "-2" and o["supports"] == "0"
+
+
+def test_set_rows_node(exe):
+    """A batched-decode cache write node: supported; a non-integer row-id
+    tensor is not; a node without row ids is rejected without a launch."""
+    o = run(exe)
+    assert o["set_rows_supports"] == "1"
+    assert o["set_rows_bad_ids"] == "0"
+    assert o["set_rows_no_ids"] == "0 -1"
