@@ -9,8 +9,13 @@
 //
 // Work decomposition.  One workgroup = 4 waves = 128 consecutive queries of
 // one (batch, q head); each wave owns 32 queries.  The workgroup walks the
-// keys in 64-key tiles staged in LDS, double-buffered: while tile n is
-// being multiplied, tile n+1 is already in flight from HBM into registers.
+// keys in 64-key tiles that buffer_load ... lds DMA copies straight from HBM
+// into LDS, double-buffered: while tile n is being multiplied, tile n+1 is in
+// flight (the first one is issued before Q is loaded).  Workgroups go
+// round-robin to the 8 XCDs; the job index is remapped so that each XCD runs
+// one contiguous block of jobs ordered (batch, KV head), then q tile (longest
+// causal rows first), then the q heads of the GQA group, and the K/V stream
+// of a KV head stays in one XCD's L2.
 //
 //   S^T[64 keys x 32 q] = K_tile . Q^T      v_mfma_f32_32x32x16_{f16,bf16}
 //                                            (A = K rows from LDS, B = Q^T
@@ -19,13 +24,18 @@
 //   column, so the row max/sum need a single cross-lane step (lane ^ 32)
 //   O^T[128 x 32 q] += V^T_tile . P^T       same MFMA; P^T comes straight
 //                                            from the S^T accumulator layout,
-//                                            V^T from the transposed LDS tile
+//                                            V^T from the row-major V tile
+//                                            through ds_read_b64_tr_b16
 //
-// LDS tiles (16 KB each, XOR-swizzled so that the staging writes and the
-// MFMA operand reads are bank-conflict free):
-//   K   [64 keys][128 dims]  16-byte chunk c of key k at slot c ^ (k & 15)
-//   V^T [128 dims][64 keys]  8-byte chunk c (4 keys) of dim d at slot
-//                            c ^ ((d & 15) ^ ((d >> 4) & 7))
+// Within a tile the two 32-key halves are software-pipelined: the QK MFMAs
+// of the second half overlap the softmax of the first, and the PV MFMAs of
+// the first overlap the softmax of the second.
+//
+// LDS tiles (16 KB each, rows of 256 B, 16-byte chunks XOR-swizzled so that
+// the DMA writes, the K operand reads and the V transpose reads are
+// bank-conflict free):
+//   K [64 keys][128 dims]  chunk c of key k at slot c ^ swz_k(k)
+//   V [64 keys][128 dims]  chunk c of key k at slot c ^ swz_v(k)
 //
 // Masks are data, not structure: a classifier pass (mask_classify_kernel)
 // labels every (128-query x 64-key) tile of the mask as all -inf (skipped:
@@ -48,39 +58,60 @@ constexpr uint32_t kXcds = 8;                // MI355X: workgroups go round-robi
 
 __global__ void __launch_bounds__(256) mask_classify_kernel(const FaArgs a, uint8_t *cls) {
     // One workgroup per (key tile, query tile, mask plane).  Each row of the
-    // tile (64 keys = 128 B) is read by 16 lanes with 8-byte loads; the
-    // prefill path guarantees 8-byte aligned mask rows.
+    // tile (64 keys = 128 B) is read by 16 lanes with 8-byte loads (the
+    // prefill path guarantees 8-byte aligned mask rows).  All 8 loads of a
+    // lane are issued before any is looked at: addresses are clamped into
+    // the live rows and keys, so no load needs a branch, and rows / keys
+    // outside [0, Sq) x [0, Skv) are excluded afterwards by predicates.  The
+    // loads go through a buffer resource over the mask plane.
     const int kt = blockIdx.x, qt = blockIdx.y, plane = blockIdx.z;
     const int m2i = plane % a.m_ne2, m3i = plane / a.m_ne2;
-    const char *base = a.mask + (int64_t)m2i * a.m_nb2 + (int64_t)m3i * a.m_nb3;
+    // (the plane base is uniform; readfirstlane lets the compiler know, so
+    // the buffer loads need no waterfall loop.  readfirstlane returns a
+    // signed int: each half is taken as uint32_t before it is widened, or a
+    // low word >= 2^31 would sign-extend over the high word)
+    const uint64_t boff = (uint64_t)((int64_t)m2i * a.m_nb2 + (int64_t)m3i * a.m_nb3);
+    const uint64_t bu = (uint64_t)(uintptr_t)a.mask + boff;
+    const uint32_t b_lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)bu);
+    const uint32_t b_hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(bu >> 32));
+    const char *base = (const char *)(uintptr_t)(((uint64_t)b_hi << 32) | (uint64_t)b_lo);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)a.m_plane_bytes, 0x00020000);
     const int q_lo = qt * kPfBM, k_lo = kt * kPfBN;
     const int c4 = threadIdx.x & 15;           // 4-key group within the row
     const int r0 = threadIdx.x >> 4;           // 16 rows per pass
     const int k = k_lo + 4 * c4;
-    int all_ninf = 1, all_zero = 1;
+    // a group starting at or past Skv is read at the last live group
+    // instead (its values are excluded below); with the mask's ne0 % 4 == 0
+    // (host-checked) every group read lies inside its row
+    const uint32_t kc = (uint32_t)min(k, (a.Skv - 1) & ~3);
+    u16x4 v[kPfBM / 16];
 #pragma unroll
     for (int pass = 0; pass < kPfBM / 16; pass++) {
-        const int q = q_lo + r0 + 16 * pass;
-        if (q >= a.Sq || k >= a.Skv) continue;
-        const uint16_t *row = (const uint16_t *)(base + (int64_t)q * a.m_nb1);
-        if (k + 3 < a.Skv) {
-            const u16x4 v = *(const u16x4 *)(row + k);
+        const uint32_t q = (uint32_t)min(q_lo + r0 + 16 * pass, a.Sq - 1);
+        v[pass] = __builtin_bit_cast(u16x4, __builtin_amdgcn_raw_buffer_load_b64(
+                                                rs, q * (uint32_t)a.m_nb1 + 2u * kc, 0, 0));
+    }
+    bool all_ninf = true, all_zero = true;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                all_ninf &= (v[i] == 0xFC00u);
-                all_zero &= ((v[i] & 0x7FFFu) == 0);
-            }
-        } else {
-            for (int i = 0; i < 4 && k + i < a.Skv; i++) {
-                const uint16_t v = row[k + i];
-                all_ninf &= (v == 0xFC00u);
-                all_zero &= ((v & 0x7FFFu) == 0);
-            }
+    for (int pass = 0; pass < kPfBM / 16; pass++) {
+        const bool row_ok = q_lo + r0 + 16 * pass < a.Sq;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const bool ok = row_ok & (k + i < a.Skv);
+            all_ninf &= !ok | (v[pass][i] == 0xFC00u);
+            all_zero &= !ok | ((v[pass][i] & 0x7FFFu) == 0);
         }
     }
-    all_ninf = __syncthreads_and(all_ninf);
-    all_zero = __syncthreads_and(all_zero);
-    if (threadIdx.x == 0) cls[((int64_t)plane * a.n_qt + qt) * a.n_kt_pad + kt] = all_ninf ? 0 : (all_zero ? 1 : 2);
+    // wave votes, then one barrier across the 4 waves
+    __shared__ uint32_t votes[4];
+    const uint64_t bad_ninf = __ballot(!all_ninf), bad_zero = __ballot(!all_zero);
+    if ((threadIdx.x & 63) == 0) votes[threadIdx.x >> 6] = (bad_ninf ? 1u : 0u) | (bad_zero ? 2u : 0u);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t any = votes[0] | votes[1] | votes[2] | votes[3];
+        cls[((int64_t)plane * a.n_qt + qt) * a.n_kt_pad + kt] = !(any & 1u) ? 0 : (!(any & 2u) ? 1 : 2);
+    }
 }
 
 // Tile classes of one (plane, query tile) row live in registers: lane l

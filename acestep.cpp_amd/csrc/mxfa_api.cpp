@@ -272,12 +272,15 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     a.mask_vec16 = a.mask_vec4 && mask->ne[0] >= 16;
     // prefill: mask rows are read in 8-byte groups of 4 keys (rows 8-byte
     // aligned) through a buffer resource over one mask plane, addressed
-    // with 32-bit offsets
+    // with 32-bit offsets.  With ne0 % 4 == 0 every group that starts below
+    // Skv lies wholly inside its row, so no load that carries a live key
+    // crosses the end of the plane (a contiguous 8-byte aligned mask has
+    // ne0 % 4 == 0 anyway; other strided views go to the decode kernel).
     if (mask) {
         const uint64_t plane = (uint64_t)(mask->ne[1] - 1) * mask->nb[1] + 2 * (uint64_t)mask->ne[0];
         a.m_plane_bytes = plane <= 0x7FFFFFFFull ? (uint32_t)plane : 0;
     }
-    const bool mask_vec_ok = !mask || (a.mask_al8 && a.m_plane_bytes != 0);
+    const bool mask_vec_ok = !mask || (a.mask_al8 && a.m_plane_bytes != 0 && mask->ne[0] % 4 == 0);
     const int64_t n_kt = (a.Skv + kPfBN - 1) / kPfBN;
     // the prefill kernel addresses one (batch, kv head)'s K and V rows with
     // 32-bit offsets from a buffer base: every row of every key tile must

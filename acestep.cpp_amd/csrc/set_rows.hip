@@ -15,13 +15,18 @@
 //
 // The op is a bandwidth-bound scatter: one thread converts 4 consecutive
 // values (one 16-byte load) and writes them to the destination row; a Q8_0
-// block is 8 threads of one wave, whose amax is a 3-step shuffle max.  Rows
+// block is 8 threads of one wave, whose amax is a 3-step DPP max.  Rows
 // whose id is out of range ([0, dst ne1)) are skipped (ggml aborts on them).
 
 #include "mxfa_common.h"
 #include "mxfa_internal.h"
 
 namespace mxfa {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
 
 template <int DT>
 __global__ void __launch_bounds__(256) set_rows_kernel(const SetRowsArgs a) {
@@ -34,20 +39,27 @@ __global__ void __launch_bounds__(256) set_rows_kernel(const SetRowsArgs a) {
     const uint32_t i02 = i23 % a.ne02, i03 = i23 / a.ne02;
     const char *ip = a.rows + (int64_t)i01 * a.r_nb0 + (int64_t)(i02 % a.r_ne1) * a.r_nb1 +
                      (int64_t)(i03 % a.r_ne2) * a.r_nb2;
+    // the source row does not depend on the row id: both loads are issued
+    // together, so a thread waits for one memory round trip, not two
+    f32x4 x = {0.f, 0.f, 0.f, 0.f};
     int64_t idx = -1;
-    if (active) idx = a.rows_i64 ? *(const int64_t *)ip : (int64_t)*(const int32_t *)ip;
+    if (active) {
+        x = *(const f32x4 *)(a.src + (int64_t)i01 * a.s_nb1 + (int64_t)i02 * a.s_nb2 + (int64_t)i03 * a.s_nb3 +
+                             16 * c);
+        idx = a.rows_i64 ? *(const int64_t *)ip : (int64_t)*(const int32_t *)ip;
+    }
     const bool ok = idx >= 0 && idx < a.dst_ne1;
-    const f32x4 x = ok ? *(const f32x4 *)(a.src + (int64_t)i01 * a.s_nb1 + (int64_t)i02 * a.s_nb2 +
-                                          (int64_t)i03 * a.s_nb3 + 16 * c)
-                       : f32x4{0.f, 0.f, 0.f, 0.f};
     char *drow = a.dst + (ok ? idx : 0) * a.d_nb1 + (int64_t)i02 * a.d_nb2 + (int64_t)i03 * a.d_nb3;
     if constexpr (DT == T_Q8_0) {
         // block of 32 values = chunks 8b .. 8b+7 = 8 consecutive lanes (a
         // row holds a multiple of 8 chunks, so blocks never straddle rows)
+        // max over the 8 lanes with DPP moves: quad_perm [1,0,3,2] and
+        // [2,3,0,1] give each quad its max, row_half_mirror (lane i <- 7-i
+        // within 8 lanes) brings in the other quad's
         float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-        amax = fmaxf(amax, __shfl_xor(amax, 1));
-        amax = fmaxf(amax, __shfl_xor(amax, 2));
-        amax = fmaxf(amax, __shfl_xor(amax, 4));
+        amax = fmaxf(amax, dpp_f32<0xB1>(amax));
+        amax = fmaxf(amax, dpp_f32<0x4E>(amax));
+        amax = fmaxf(amax, dpp_f32<0x141>(amax));
         if (!ok) return;
         const float d = amax / 127.0f;
         const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
