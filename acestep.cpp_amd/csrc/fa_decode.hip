@@ -67,6 +67,7 @@ constexpr int kMaskNone = 0;     // no mask
 constexpr int kMaskVec = 1;      // 8-byte aligned rows of >= round_up(Skv, 4) entries (LDS
                                  // kernel: and >= 16)
 constexpr int kMaskScalar = 2;   // anything else
+constexpr int kMaskStruct = 3;   // structured mask (a.sm_*): no mask reads
 
 // Per-lane coordinates of a decode workgroup.
 struct Tile {
@@ -94,6 +95,38 @@ __device__ __forceinline__ Tile make_tile(const FaArgs &a) {
     t.iq1 = t.row_ok ? t.r / a.G : 0;
     t.head = t.kvh * a.G + (t.row_ok ? t.r % a.G : 0);
     return t;
+}
+
+// Key range [k0, k1) of this workgroup's split, and the number of splits
+// `ns` of its (batch, kv head, row tile) stream.  Dense masks: splits of
+// a.chunk keys from 0 (a.n_splits of them).  Structured masks: splits of
+// a.chunk keys from the first key any row of the tile sees, up to the last
+// one (the host sized a.chunk from the live lengths, so splits carry equal
+// work); workgroups past the stream's last split do nothing (skip).
+struct SplitRange {
+    int k0, k1, ns;
+    bool skip;
+};
+template <int MM>
+__device__ __forceinline__ SplitRange split_range(const FaArgs &a, const Tile &t) {
+    SplitRange sr;
+    if constexpr (MM == kMaskStruct) {
+        const int r0 = t.rt * 16, nr = min(16, a.M - r0);
+        int lo_f, hi_f, lo_l, hi_l;
+        sm_row_range(a, t.b, r0 / a.G, lo_f, hi_f);
+        sm_row_range(a, t.b, (r0 + nr - 1) / a.G, lo_l, hi_l);
+        const int len = max(0, hi_l - lo_f);
+        sr.ns = max(1, (len + a.chunk - 1) / a.chunk);
+        sr.skip = t.split >= sr.ns;
+        sr.k0 = len ? lo_f + t.split * a.chunk : 0;
+        sr.k1 = len ? min(hi_l, sr.k0 + a.chunk) : 0;
+    } else {
+        sr.ns = a.n_splits;
+        sr.skip = false;
+        sr.k0 = t.split * a.chunk;
+        sr.k1 = min(a.Skv, sr.k0 + a.chunk);
+    }
+    return sr;
 }
 
 __device__ __forceinline__ const float *q_row(const FaArgs &a, const Tile &t) {
@@ -208,8 +241,8 @@ __device__ __forceinline__ float ld_dev(const float *p) {
 // phase B has each thread accumulate one dim of a few rows over all splits
 // with batches of independent loads (one memory round trip per batch).
 constexpr int kMaxSplits = 64;
-__device__ void merge_splits(const FaArgs &a, const Tile &t, int64_t pr0, int nr, float *lds) {
-    const int ns = a.n_splits;
+__device__ void merge_splits(const FaArgs &a, const Tile &t, int64_t pr0, int nr, int ns, float *lds) {
+    const int stride = a.n_splits;            // partial slots per row
     float *wm = lds;                         // [16][kMaxSplits]: m, then weights
     float *wl = wm + 16 * kMaxSplits;        // [16][kMaxSplits]: l
     float *Linv = wl + 16 * kMaxSplits;      // [16]
@@ -220,7 +253,7 @@ __device__ void merge_splits(const FaArgs &a, const Tile &t, int64_t pr0, int nr
         for (int u = 0; u < 4; u++) {
             const int i = i0 + t.tid + 256 * u;
             const int r = i / ns, sp = i - r * ns;
-            const float *pm = a.part_ml + ((pr0 + r) * ns + sp) * 2;
+            const float *pm = a.part_ml + ((pr0 + r) * stride + sp) * 2;
             mv[u] = i < nr * ns ? ld_dev(pm) : 0.0f;
             lv[u] = i < nr * ns ? ld_dev(pm + 1) : 0.0f;
         }
@@ -252,7 +285,7 @@ __device__ void merge_splits(const FaArgs &a, const Tile &t, int64_t pr0, int nr
     // phase B: thread -> dim t.tid % 128, rows t.tid / 128 + 2j
     const int d = t.tid & (kD - 1);
     for (int r = t.tid >> 7; r < nr; r += 2) {
-        const float *po = a.part_o + (pr0 + r) * ns * kD + d;
+        const float *po = a.part_o + (pr0 + r) * stride * kD + d;
         float acc = 0.0f;
         for (int s0 = 0; s0 < ns; s0 += 16) {
             float ov[16];
@@ -274,8 +307,8 @@ __device__ void merge_splits(const FaArgs &a, const Tile &t, int64_t pr0, int nr
 // once every wave has passed the first barrier.  o[dt][i] =
 // O^T[16dt + 4*g16 + i][row c16] (unnormalised), m2 in the exp2 domain,
 // lsum the lane's share of the row sum.
-__device__ void finish_tile(const FaArgs &a, const Tile &t, const f32x4 (&o)[8], float m2, float lsum, float *lds,
-                            int *last_lds) {
+__device__ void finish_tile(const FaArgs &a, const Tile &t, int ns, const f32x4 (&o)[8], float m2, float lsum,
+                            float *lds, int *last_lds) {
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
     __syncthreads();
@@ -320,7 +353,7 @@ __device__ void finish_tile(const FaArgs &a, const Tile &t, const f32x4 (&o)[8],
     }
     const int iq1o = rglob / a.G, heado = t.kvh * a.G + rglob % a.G;
     float *dp = a.dst + (((int64_t)t.b * a.Sq + iq1o) * a.Nh + heado) * kD + dd0;
-    if (a.n_splits == 1) {
+    if (ns == 1) {
         if (!out_row) return;
         const float inv = (L == 0.0f) ? 0.0f : 1.0f / L;
         *(f32x4 *)dp = f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
@@ -350,12 +383,12 @@ __device__ void finish_tile(const FaArgs &a, const Tile &t, const f32x4 (&o)[8],
     __syncthreads();
     if (t.tid == 0) {
         const int prev = __hip_atomic_fetch_add(&a.tickets[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *last_lds = prev == a.n_splits - 1;
+        *last_lds = prev == ns - 1;
     }
     __syncthreads();
     if (!*last_lds) return;
     if (t.tid == 0) __hip_atomic_store(&a.tickets[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    merge_splits(a, t, pr0, min(16, a.M - t.rt * 16), lds);
+    merge_splits(a, t, pr0, min(16, a.M - t.rt * 16), ns, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -407,7 +440,7 @@ __device__ __forceinline__ void wait_stages(int n) {
 template <int KT, int MM, int NST>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 fa_decode_lds_kernel(const FaArgs a) {
-    static_assert(MM == kMaskNone || MM == kMaskVec, "mask mode");
+    static_assert(MM == kMaskNone || MM == kMaskVec || MM == kMaskStruct, "mask mode");
     static_assert(NST >= 2 && NST <= 4, "stages");
     using MF = Mfma16<KT>;
     using V8 = typename MF::v8;
@@ -420,6 +453,8 @@ fa_decode_lds_kernel(const FaArgs a) {
     __shared__ int last_lds;
 
     const Tile t = make_tile(a);
+    const SplitRange sr = split_range<MM>(a, t);
+    if (sr.skip) return;   // past the stream's last split (uniform: no waits, no LDS, no ticket)
     const int lane = t.lane, c16 = t.c16, g16 = t.g16;
     V8 qb[4];
     load_q16<KT>(a, t, qb);
@@ -430,9 +465,11 @@ fa_decode_lds_kernel(const FaArgs a) {
     const bool use_softcap = a.softcap != 0.0f;
     const float sc_in = a.softcap_in;
     const int skv4 = (a.Skv + 3) & ~3;
-    const int k0 = t.split * a.chunk;
-    const int k1 = min(a.Skv, k0 + a.chunk);
+    const int k0 = sr.k0, k1 = sr.k1;
     uint8_t *ring = smem + t.wave * NST * kStBytes;
+    // structured mask: the live keys of this lane's row
+    int rlo = 0, rhi = 0;
+    if constexpr (MM == kMaskStruct) sm_row_range(a, t.b, t.iq1, rlo, rhi);
 
     // DMA lane geometry.  K/V: instruction j covers keys 4j..4j+3 of the
     // stage, lane -> (key 4j + lane/16, slot lane%16).  Mask: instruction i
@@ -507,7 +544,8 @@ fa_decode_lds_kernel(const FaArgs a) {
         for (int i = 0; i < 4; i++) {
             const int key = kb + 4 * g16 + i;
             float mv = -INFINITY;
-            if (t.row_ok && key < hi) mv = MM == kMaskVec ? h2f_bits(mw[i]) * slope_l2 : 0.0f;
+            const bool in_row = MM != kMaskStruct || (key >= rlo && key < rhi);
+            if (t.row_ok && key < hi && in_row) mv = MM == kMaskVec ? h2f_bits(mw[i]) * slope_l2 : 0.0f;
             mk[i] = mv;
             live |= (mv != -INFINITY);
         }
@@ -593,7 +631,7 @@ fa_decode_lds_kernel(const FaArgs a) {
         MXFA_WAIT_LGKMCNT0();   // this slot's LDS reads are done before it is refilled
     }
     MXFA_WAIT_VMCNT(0);
-    finish_tile(a, t, o, m2, lsum, (float *)smem, &last_lds);
+    finish_tile(a, t, sr.ns, o, m2, lsum, (float *)smem, &last_lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -663,6 +701,8 @@ fa_decode_reg_kernel(const FaArgs a) {
     __shared__ int last_lds;
 
     const Tile t = make_tile(a);
+    const SplitRange sr = split_range<MM>(a, t);
+    if (sr.skip) return;   // past the stream's last split (uniform: no waits, no LDS, no ticket)
     const int c16 = t.c16, g16 = t.g16;
     V8 qb[4];
     long qq[4];
@@ -670,7 +710,8 @@ fa_decode_reg_kernel(const FaArgs a) {
     if constexpr (kQ8) load_q8(a, t, qq, dq);
     else load_q16<TV>(a, t, qb);
     const float slope_l2 = alibi_slope(a, t.head) * kLog2e;
-    const uint16_t *mrow = MM != kMaskNone ? mask_row(a, t.iq1, t.head, t.b) : nullptr;
+    constexpr bool kDense = MM == kMaskVec || MM == kMaskScalar;   // a dense mask is read
+    const uint16_t *mrow = kDense ? mask_row(a, t.iq1, t.head, t.b) : nullptr;
     const int skv4 = (a.Skv + 3) & ~3;
     const char *kbase = a.k + (int64_t)t.kvh * a.k_nb2 + (int64_t)t.bk * a.k_nb3;
     const char *vbase = a.v + (int64_t)t.kvh * a.v_nb2 + (int64_t)t.bk * a.v_nb3;
@@ -678,10 +719,11 @@ fa_decode_reg_kernel(const FaArgs a) {
     const bool use_softcap = a.softcap != 0.0f;
     const float sc_in = a.softcap_in;
 
-    const int k0 = t.split * a.chunk;
-    const int k1 = min(a.Skv, k0 + a.chunk);
+    const int k0 = sr.k0, k1 = sr.k1;
     int lo = k0, hi = k1;
-    if constexpr (MM != kMaskNone) live_range(a, t, k0, k1, range_lds, lo, hi);
+    if constexpr (kDense) live_range(a, t, k0, k1, range_lds, lo, hi);
+    int rlo = 0, rhi = 0;
+    if constexpr (MM == kMaskStruct) sm_row_range(a, t.b, t.iq1, rlo, rhi);
 
     f32x4 o[8];
 #pragma unroll
@@ -740,7 +782,8 @@ fa_decode_reg_kernel(const FaArgs a) {
             for (int i = 0; i < 4; i++) {
                 const int key = kb + 16 * sb + 4 * g16 + i;
                 float mv = -INFINITY;
-                if (t.row_ok && key < hi) mv = MM != kMaskNone ? h2f_bits(x.m[sb][i]) * slope_l2 : 0.0f;
+                const bool in_row = MM != kMaskStruct || (key >= rlo && key < rhi);
+                if (t.row_ok && key < hi && in_row) mv = kDense ? h2f_bits(x.m[sb][i]) * slope_l2 : 0.0f;
                 mk[sb][i] = mv;
                 live |= (mv != -INFINITY);
             }
@@ -902,7 +945,7 @@ fa_decode_reg_kernel(const FaArgs a) {
             }
         }
     }
-    finish_tile(a, t, o, m2, lsum, (float *)vt_lds, &last_lds);
+    finish_tile(a, t, sr.ns, o, m2, lsum, (float *)vt_lds, &last_lds);
 }
 
 // Zero-fill of the split tickets (run when the ticket buffer is created or
@@ -938,11 +981,13 @@ static hipError_t launch_lds(const FaArgs &a, dim3 grid, hipStream_t stream) {
 template <int KT>
 static hipError_t launch_typed(const FaArgs &a, dim3 grid, hipStream_t stream) {
     if constexpr (KT != T_Q8_0) {
+        if (a.sm_flags) return launch_lds<KT, kMaskStruct>(a, grid, stream);
         if (!a.mask) return launch_lds<KT, kMaskNone>(a, grid, stream);
         if (a.mask_vec16) return launch_lds<KT, kMaskVec>(a, grid, stream);
         hipLaunchKernelGGL((fa_decode_reg_kernel<KT, kMaskScalar>), grid, dim3(256), 0, stream, a);
     } else {
-        if (!a.mask) hipLaunchKernelGGL((fa_decode_reg_kernel<KT, kMaskNone>), grid, dim3(256), 0, stream, a);
+        if (a.sm_flags) hipLaunchKernelGGL((fa_decode_reg_kernel<KT, kMaskStruct>), grid, dim3(256), 0, stream, a);
+        else if (!a.mask) hipLaunchKernelGGL((fa_decode_reg_kernel<KT, kMaskNone>), grid, dim3(256), 0, stream, a);
         else if (a.mask_vec4) hipLaunchKernelGGL((fa_decode_reg_kernel<KT, kMaskVec>), grid, dim3(256), 0, stream, a);
         else hipLaunchKernelGGL((fa_decode_reg_kernel<KT, kMaskScalar>), grid, dim3(256), 0, stream, a);
     }

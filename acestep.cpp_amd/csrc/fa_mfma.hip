@@ -205,8 +205,10 @@ __device__ __forceinline__ void scale_acc(f32x16 &o, float alpha) {
 enum : int { kSgMfma = 0x008, kSgValu = 0x402, kSgDsRead = 0x100 };
 
 // CAP: logit softcap on (a per-call constant; its tanh path is compiled only
-// into the instances that need it, so it costs the common path no registers)
-template <int T, bool CAP>
+// into the instances that need it, so it costs the common path no registers).
+// SM: structured mask (a.sm_*): tile classes and per-element liveness are
+// arithmetic on (query row, key) -- no classifier pass, no mask reads.
+template <int T, bool CAP, bool SM>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fa_prefill_kernel(const FaArgs a) {
     using MF = Mfma32<T>;
@@ -240,15 +242,44 @@ fa_prefill_kernel(const FaArgs a) {
     const int qrow = qt * kPfBM + wave * 32 + l32;
     const bool row_ok = qrow < a.Sq;
     const int qrow_c = row_ok ? qrow : a.Sq - 1;
-
+    // Structured mask: the tile's rows together cover keys [lo(first row),
+    // hi(last row)) -- key tiles outside are skipped -- and every row sees
+    // [lo(last row), hi(first row)) = [sm_in_lo, sm_in_hi): a key tile in
+    // there needs no per-element test (class 1); the others test each key
+    // against the lane's own row range [row_lo, row_hi).
+    int sm_kt_first = 0, sm_kt_end = 0, sm_in_lo = 0, sm_in_hi = 0, row_lo = 0, row_hi = 0;
+    if constexpr (SM) {
+        const int q_first = qt * kPfBM, q_last = min(q_first + kPfBM, a.Sq) - 1;
+        int lo_f, hi_f, lo_l, hi_l;
+        sm_row_range(a, b, q_first, lo_f, hi_f);
+        sm_row_range(a, b, q_last, lo_l, hi_l);
+        sm_kt_first = __builtin_amdgcn_readfirstlane(max(lo_f, 0) / kPfBN);
+        sm_kt_end = __builtin_amdgcn_readfirstlane(lo_f < hi_l ? (hi_l + kPfBN - 1) / kPfBN : 0);
+        sm_in_lo = __builtin_amdgcn_readfirstlane(lo_l);
+        sm_in_hi = __builtin_amdgcn_readfirstlane(hi_f);
+        sm_row_range(a, b, qrow_c, row_lo, row_hi);
+    }
     const int plane = a.mask ? (b % a.m_ne3) * a.m_ne2 + head % a.m_ne2 : 0;
-    TileClasses tc{0u, 0u, a.tile_class != nullptr};
+    TileClasses tc{0u, 0u, !SM && a.tile_class != nullptr};
     if (tc.present) {
         const uint32_t *row = (const uint32_t *)(a.tile_class + ((int64_t)plane * a.n_qt + qt) * a.n_kt_pad);
         const int lane4 = 4 * lane;
         if (lane4 < a.n_kt) tc.w0 = row[lane4 >> 2];
         if (256 + lane4 < a.n_kt) tc.w1 = row[(256 + lane4) >> 2];
     }
+    // first live key tile at or after kt (n_kt: none), and a tile's class
+    auto next_live = [&](int kt) __attribute__((always_inline)) -> int {
+        if constexpr (SM) {
+            const int k = max(kt, sm_kt_first);
+            return k < sm_kt_end ? k : a.n_kt;
+        } else {
+            return tc.next_live(kt, a.n_kt);
+        }
+    };
+    auto class_of = [&](int kt) __attribute__((always_inline)) -> int {
+        if constexpr (SM) return (kt * kPfBN >= sm_in_lo && kt * kPfBN + kPfBN <= sm_in_hi) ? 1 : 2;
+        else return tc.at(kt);
+    };
     // Mask rows of this (batch, head) plane through a buffer resource: lane
     // offset qrow * nb1 + 2 * key (32-bit, the host checks the plane size);
     // reads past the plane return zeros, so 4-key groups at the row end need
@@ -310,7 +341,7 @@ fa_prefill_kernel(const FaArgs a) {
 
     // The first live tile's copies go out before Q is loaded: the two
     // fetches share one memory latency.
-    int kt = tc.next_live(0, n_kt);
+    int kt = next_live(0);
     if (kt < n_kt) issue(kt, std::integral_constant<int, 0>{});
 
     // Q^T operand for the 8 dim-steps of 16: Q[qrow][16t + 8h + e].
@@ -372,6 +403,22 @@ fa_prefill_kernel(const FaArgs a) {
     // general tile: on a tile of class 1 it is all zero, and without a mask
     // the resource is empty (reads return zero), so no branch is needed.
     auto general_x = [&](f32x16 &sc, int key0) __attribute__((always_inline)) {
+        if constexpr (SM) {
+            // live keys 8j + i of [lo_rel, hi_rel) (row_hi <= Skv); the
+            // zero mask value keeps the arithmetic of the dense path
+            const int lo_rel = row_lo - key0 - 4 * h, hi_rel = row_hi - key0 - 4 * h;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 4 * j + i, off = 8 * j + i;
+                    float x;
+                    if constexpr (CAP) x = (a.softcap * fast_tanh(sc[r] * sc_in)) * kLog2e + 0.0f;
+                    else x = fmaf(sc[r], sl2, 0.0f);
+                    sc[r] = (off >= lo_rel && off < hi_rel) ? x : -INFINITY;
+                }
+            return;
+        }
         const int kmax = a.Skv - key0 - 4 * h;   // keys 8j + i >= kmax lie past Skv
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -415,7 +462,7 @@ fa_prefill_kernel(const FaArgs a) {
     // The code is laid out in issue order; sched_barrier fences keep it.
     // Operand reads run two MFMAs ahead.
     auto tile = [&](auto st_c, int kt) __attribute__((always_inline)) {
-        const int cl = __builtin_amdgcn_readfirstlane(tc.at(kt));
+        const int cl = __builtin_amdgcn_readfirstlane(class_of(kt));
         const int key0 = kt * kPfBN;
         const bool general =
             __builtin_amdgcn_readfirstlane((int)(cl == 2 || key0 + kPfBN > a.Skv || !lean_ok)) != 0;
@@ -505,14 +552,14 @@ fa_prefill_kernel(const FaArgs a) {
     std::integral_constant<int, 0> st0;
     std::integral_constant<int, 1> st1;
     while (kt < n_kt) {
-        int kn = tc.next_live(kt + 1, n_kt);
+        int kn = next_live(kt + 1);
         MXFA_WAIT_VMCNT(0);
         __builtin_amdgcn_s_barrier();
         if (kn < n_kt) issue(kn, st1);
         tile(st0, kt);
         kt = kn;
         if (kt >= n_kt) break;
-        kn = tc.next_live(kt + 1, n_kt);
+        kn = next_live(kt + 1);
         MXFA_WAIT_VMCNT(0);
         __builtin_amdgcn_s_barrier();
         if (kn < n_kt) issue(kn, st0);
@@ -543,16 +590,18 @@ hipError_t launch_mask_classify(const FaArgs &a, int n_planes, uint8_t *classes,
 
 hipError_t launch_fa_prefill(const FaArgs &a, int ktype, hipStream_t stream) {
     dim3 grid((uint32_t)a.n_qt * (uint32_t)a.Nh * (uint32_t)a.B);
-    const bool cap = a.softcap != 0.0f;
+    const bool cap = a.softcap != 0.0f, sm = a.sm_flags != 0;
+#define MXFA_PF(TT, C, S) hipLaunchKernelGGL((fa_prefill_kernel<TT, C, S>), grid, dim3(256), kPfLds, stream, a)
     if (ktype == T_F16) {
-        if (cap) hipLaunchKernelGGL((fa_prefill_kernel<T_F16, true>), grid, dim3(256), kPfLds, stream, a);
-        else hipLaunchKernelGGL((fa_prefill_kernel<T_F16, false>), grid, dim3(256), kPfLds, stream, a);
+        if (sm) { if (cap) MXFA_PF(T_F16, true, true); else MXFA_PF(T_F16, false, true); }
+        else { if (cap) MXFA_PF(T_F16, true, false); else MXFA_PF(T_F16, false, false); }
     } else if (ktype == T_BF16) {
-        if (cap) hipLaunchKernelGGL((fa_prefill_kernel<T_BF16, true>), grid, dim3(256), kPfLds, stream, a);
-        else hipLaunchKernelGGL((fa_prefill_kernel<T_BF16, false>), grid, dim3(256), kPfLds, stream, a);
+        if (sm) { if (cap) MXFA_PF(T_BF16, true, true); else MXFA_PF(T_BF16, false, true); }
+        else { if (cap) MXFA_PF(T_BF16, true, false); else MXFA_PF(T_BF16, false, false); }
     } else {
         return hipErrorInvalidValue;
     }
+#undef MXFA_PF
     return hipGetLastError();
 }
 

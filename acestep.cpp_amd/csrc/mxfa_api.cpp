@@ -224,9 +224,41 @@ int check(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, cons
     return MXFA_OK;
 }
 
+// Validation of a structured mask (mxfa_mask_spec) for q's shape.
+int check_spec(const mxfa_mask_spec *sm, const mxfa_tensor *q) {
+    if (!sm) return fail(MXFA_ERR_INVALID, "mask spec is required");
+    if (sm->flags & ~(MXFA_MASK_CAUSAL | MXFA_MASK_WINDOW | MXFA_MASK_LENGTHS))
+        return fail(MXFA_ERR_INVALID, "unknown mask flags 0x%x", sm->flags);
+    const int64_t lim = (int64_t)1 << 30;
+    const int64_t w = (sm->flags & MXFA_MASK_WINDOW) ? sm->window : 0;
+    if (w < 0) return fail(MXFA_ERR_INVALID, "window %d < 0", sm->window);
+    if (sm->pos0 < 0 || sm->pos0 + q->ne[1] + w >= lim) return fail(MXFA_ERR_INVALID, "pos0 / window out of range");
+    if (sm->flags & MXFA_MASK_LENGTHS) {
+        if (!sm->lengths) return fail(MXFA_ERR_INVALID, "MXFA_MASK_LENGTHS without lengths");
+        if (sm->n_lengths != 1 && sm->n_lengths != q->ne[3])
+            return fail(MXFA_ERR_INVALID, "n_lengths %d must be 1 or B = %lld", sm->n_lengths, (long long)q->ne[3]);
+        if (sm->n_lengths > kSmMaxLen)
+            return fail(MXFA_ERR_UNSUPPORTED, "n_lengths %d > %d", sm->n_lengths, kSmMaxLen);
+        for (int i = 0; i < sm->n_lengths; i++)
+            if (sm->lengths[i] < 0) return fail(MXFA_ERR_INVALID, "lengths[%d] = %d < 0", i, sm->lengths[i]);
+    }
+    return MXFA_OK;
+}
+
 void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
-               const mxfa_params *p, mxfa_tensor *dst, Plan &pl) {
+               const mxfa_params *p, mxfa_tensor *dst, Plan &pl, const mxfa_mask_spec *sm = nullptr) {
     FaArgs &a = pl.args;
+    if (sm && sm->flags) {
+        a.sm_flags = sm->flags;
+        a.sm_window = (sm->flags & MXFA_MASK_WINDOW) ? sm->window : 0;
+        a.sm_pos0 = (int32_t)sm->pos0;
+        a.sm_nlen = 1;
+        if (sm->flags & MXFA_MASK_LENGTHS) {
+            a.sm_nlen = sm->n_lengths;
+            for (int i = 0; i < sm->n_lengths; i++)
+                a.sm_len[i] = (int32_t)std::min<int64_t>(sm->lengths[i], k->ne[1]);
+        }
+    }
     a.q = (const char *)q->data;
     a.k = (const char *)k->data;
     a.v = (const char *)v->data;
@@ -301,12 +333,34 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     a.row_tiles = (a.M + 15) / 16;
     const int64_t base = (int64_t)a.B * a.Nkv * a.row_tiles;
     const int64_t max_splits = (a.Skv + kSplitKeyQuantum - 1) / kSplitKeyQuantum;
-    int64_t n_splits = 1;
-    if (base < kSplitTargetWgs)
-        n_splits = std::min<int64_t>({max_splits, (kSplitTargetWgs + base - 1) / base, kMaxDecodeSplits});
-    int64_t chunk = (a.Skv + n_splits - 1) / n_splits;
-    chunk = (chunk + kSplitKeyQuantum - 1) / kSplitKeyQuantum * kSplitKeyQuantum;
-    n_splits = (a.Skv + chunk - 1) / chunk;
+    int64_t n_splits = 1, chunk = 0;
+    auto round_q = [](int64_t x) { return (x + kSplitKeyQuantum - 1) / kSplitKeyQuantum * kSplitKeyQuantum; };
+    if (a.sm_flags) {
+        // Structured mask: every (batch, kv head, row tile) stream covers
+        // the keys its rows see; one chunk size for all of them, from the
+        // total live work, so that every split carries the same work.
+        int64_t total = 0, max_len = 0;
+        std::vector<int64_t> lens((size_t)a.B * a.row_tiles);
+        for (int b = 0; b < a.B; b++)
+            for (int rt = 0; rt < a.row_tiles; rt++) {
+                const int r0 = rt * 16, nr = std::min(16, a.M - r0);
+                int lo_f, hi_f, lo_l, hi_l;
+                sm_row_range(a, b, r0 / a.G, lo_f, hi_f);
+                sm_row_range(a, b, (r0 + nr - 1) / a.G, lo_l, hi_l);
+                const int64_t len = std::max(0, hi_l - lo_f);
+                lens[(size_t)b * a.row_tiles + rt] = len;
+                total += len * a.Nkv;
+                max_len = std::max(max_len, len);
+            }
+        chunk = round_q(std::max<int64_t>({(total + kSplitTargetWgs - 1) / kSplitTargetWgs,
+                                           (max_len + kMaxDecodeSplits - 1) / kMaxDecodeSplits, 1}));
+        for (int64_t len : lens) n_splits = std::max<int64_t>(n_splits, (len + chunk - 1) / chunk);
+    } else {
+        if (base < kSplitTargetWgs)
+            n_splits = std::min<int64_t>({max_splits, (kSplitTargetWgs + base - 1) / base, kMaxDecodeSplits});
+        chunk = round_q((a.Skv + n_splits - 1) / n_splits);
+        n_splits = (a.Skv + chunk - 1) / chunk;
+    }
     a.n_splits = (int32_t)n_splits;
     a.chunk = (int32_t)chunk;
     if (n_splits > 1) {
@@ -409,6 +463,43 @@ void drain_pending() {
     g_pending.clear();
 }
 
+// Plans and launches one validated call (dense `mask` or structured `sm`).
+int run(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
+        const mxfa_params *params, mxfa_tensor *dst, void *hip_stream, const mxfa_mask_spec *sm) {
+    hipStream_t stream = (hipStream_t)hip_stream;
+    Plan pl;
+    make_plan(q, k, v, mask, params, dst, pl, sm);
+    void *ws = nullptr;
+    if (!pl.prefill && (int64_t)pl.args.Nkv * pl.args.row_tiles > 65535)
+        return fail(MXFA_ERR_UNSUPPORTED, "too many query rows per KV head for the decode kernel");
+    int *tickets = nullptr;
+    int rc = ensure_workspace(pl.ws_bytes, pl.n_tickets, stream, &ws, &tickets);
+    if (rc != MXFA_OK) return rc;
+    FaArgs &a = pl.args;
+    hipError_t e;
+    if (pl.prefill) {
+        if (a.mask) {
+            uint8_t *cls = (uint8_t *)ws;
+            a.tile_class = cls;
+            e = timed_launch("mask_classify", stream,
+                             [&] { return launch_mask_classify(a, pl.n_planes, cls, stream); });
+            if (e != hipSuccess) return fail(MXFA_ERR_HIP, "mask classify launch: %s", hipGetErrorString(e));
+        }
+        e = timed_launch("fa_prefill", stream, [&] { return launch_fa_prefill(a, pl.ktype, stream); });
+        if (e != hipSuccess) return fail(MXFA_ERR_HIP, "prefill launch: %s", hipGetErrorString(e));
+        return MXFA_OK;
+    }
+    if (a.n_splits > 1) {
+        const size_t rows = (size_t)a.B * a.Nkv * a.M * a.n_splits;
+        a.part_o = (float *)ws;
+        a.part_ml = a.part_o + rows * kD;
+        a.tickets = tickets;
+    }
+    e = launch_fa_decode(a, pl.ktype, stream);
+    if (e != hipSuccess) return fail(MXFA_ERR_HIP, "decode launch: %s", hipGetErrorString(e));
+    return MXFA_OK;
+}
+
 }  // namespace
 
 namespace mxfa {
@@ -458,40 +549,32 @@ int mxfa_supports(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor 
 int mxfa_flash_attn_ext(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
                         const mxfa_params *params, mxfa_tensor *dst, void *hip_stream) {
     if (!dst) return fail(MXFA_ERR_INVALID, "dst is required");
-    int rc = check(q, k, v, mask, params, dst);
+    const int rc = check(q, k, v, mask, params, dst);
     if (rc != MXFA_OK) return rc;
-    hipStream_t stream = (hipStream_t)hip_stream;
+    return run(q, k, v, mask, params, dst, hip_stream, nullptr);
+}
+
+int mxfa_supports_masked(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_mask_spec *mask,
+                         const mxfa_params *params, const mxfa_tensor *dst) {
+    if (check(q, k, v, nullptr, params, dst) != MXFA_OK || check_spec(mask, q) != MXFA_OK) return 0;
     Plan pl;
-    make_plan(q, k, v, mask, params, dst, pl);
-    void *ws = nullptr;
-    if (!pl.prefill && (int64_t)pl.args.Nkv * pl.args.row_tiles > 65535)
-        return fail(MXFA_ERR_UNSUPPORTED, "too many query rows per KV head for the decode kernel");
-    int *tickets = nullptr;
-    rc = ensure_workspace(pl.ws_bytes, pl.n_tickets, stream, &ws, &tickets);
+    make_plan(q, k, v, nullptr, params, nullptr, pl, mask);
+    if (!pl.prefill && (int64_t)pl.args.Nkv * pl.args.row_tiles > 65535) {
+        fail(MXFA_ERR_UNSUPPORTED, "too many query rows per KV head for the decode kernel");
+        return 0;
+    }
+    return 1;
+}
+
+int mxfa_flash_attn_ext_masked(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
+                               const mxfa_mask_spec *mask, const mxfa_params *params, mxfa_tensor *dst,
+                               void *hip_stream) {
+    if (!dst) return fail(MXFA_ERR_INVALID, "dst is required");
+    int rc = check(q, k, v, nullptr, params, dst);
     if (rc != MXFA_OK) return rc;
-    FaArgs &a = pl.args;
-    hipError_t e;
-    if (pl.prefill) {
-        if (a.mask) {
-            uint8_t *cls = (uint8_t *)ws;
-            a.tile_class = cls;
-            e = timed_launch("mask_classify", stream,
-                             [&] { return launch_mask_classify(a, pl.n_planes, cls, stream); });
-            if (e != hipSuccess) return fail(MXFA_ERR_HIP, "mask classify launch: %s", hipGetErrorString(e));
-        }
-        e = timed_launch("fa_prefill", stream, [&] { return launch_fa_prefill(a, pl.ktype, stream); });
-        if (e != hipSuccess) return fail(MXFA_ERR_HIP, "prefill launch: %s", hipGetErrorString(e));
-        return MXFA_OK;
-    }
-    if (a.n_splits > 1) {
-        const size_t rows = (size_t)a.B * a.Nkv * a.M * a.n_splits;
-        a.part_o = (float *)ws;
-        a.part_ml = a.part_o + rows * kD;
-        a.tickets = tickets;
-    }
-    e = launch_fa_decode(a, pl.ktype, stream);
-    if (e != hipSuccess) return fail(MXFA_ERR_HIP, "decode launch: %s", hipGetErrorString(e));
-    return MXFA_OK;
+    rc = check_spec(mask, q);
+    if (rc != MXFA_OK) return rc;
+    return run(q, k, v, nullptr, params, dst, hip_stream, mask);
 }
 
 int mxfa_set_rows_supports(const mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_tensor *rows) {

@@ -29,6 +29,17 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
+// Structured masks (mxfa_flash_attn_ext_masked): the mask as metadata.  Key
+// j is live for query row i of batch b iff
+//   j < len[b % n_len]            (kSmLengths: padding, qwen3-lm.h:879,
+//                                  dit-sampler.h:303)
+//   j <= pos0 + i                 (kSmCausal: qwen3-lm.h:605, qwen3-enc.h:433)
+//   |pos0 + i - j| <= window      (kSmWindow: dit-sampler.h:282,
+//                                  cond-enc.h:317, :341)
+// -- the same as a dense F16 mask holding 0 there and -inf elsewhere.
+constexpr int kSmCausal = 1, kSmWindow = 2, kSmLengths = 4;
+constexpr int kSmMaxLen = 64;   // per-batch lengths carried in the arguments
+
 // Arguments shared by the attention kernels (passed by value).
 struct FaArgs {
     const char *q, *k, *v, *mask;
@@ -58,7 +69,28 @@ struct FaArgs {
     const uint8_t *tile_class;
     int32_t n_qt, n_kt;                   // tiles along Sq and Skv
     int32_t n_kt_pad;                     // class row stride (n_kt rounded up to 4)
+    // structured mask (sm_flags == 0: none; then `mask` may hold a dense one)
+    int32_t sm_flags, sm_window, sm_pos0, sm_nlen;
+    int32_t sm_len[kSmMaxLen];
 };
+
+// Live keys [lo, hi) of query row iq1 of batch b under the structured mask
+// (both ends are non-decreasing in iq1, so the rows of a tile cover
+// [lo(first row), hi(last row)) and all of them see [lo(last), hi(first))).
+__host__ __device__ __forceinline__ void sm_row_range(const FaArgs &a, int b, int iq1, int &lo, int &hi) {
+    const int p = a.sm_pos0 + iq1;
+    lo = 0;
+    hi = a.Skv;
+    if (a.sm_flags & kSmLengths) {
+        const int len = a.sm_len[b % a.sm_nlen];
+        hi = hi < len ? hi : len;
+    }
+    if (a.sm_flags & kSmCausal) hi = hi < p + 1 ? hi : p + 1;
+    if (a.sm_flags & kSmWindow) {
+        lo = lo > p - a.sm_window ? lo : p - a.sm_window;
+        hi = hi < p + a.sm_window + 1 ? hi : p + a.sm_window + 1;
+    }
+}
 
 // MFMA 16x16x32 for the two 16-bit float formats (8 k-values per lane).
 template <int T> struct Mfma16;

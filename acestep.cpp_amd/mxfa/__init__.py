@@ -38,6 +38,8 @@ OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NOMEM = 0, -1, -2, -3, -4
 EXPORTED_SYMBOLS = (
     "mxfa_supports",
     "mxfa_flash_attn_ext",
+    "mxfa_supports_masked",
+    "mxfa_flash_attn_ext_masked",
     "mxfa_set_rows_supports",
     "mxfa_set_rows",
     "mxfa_release",
@@ -68,6 +70,36 @@ class MxfaParams(ctypes.Structure):
     ]
 
 
+MASK_CAUSAL, MASK_WINDOW, MASK_LENGTHS = 1, 2, 4
+
+
+class MxfaMaskSpec(ctypes.Structure):
+    _fields_ = [
+        ("flags", ctypes.c_int32),
+        ("window", ctypes.c_int32),
+        ("pos0", ctypes.c_int64),
+        ("n_lengths", ctypes.c_int32),
+        ("lengths", ctypes.POINTER(ctypes.c_int32)),
+    ]
+
+
+def mask_spec(causal: bool = False, pos0: int = 0, window: Optional[int] = None, lengths=None):
+    """A structured mask (mxfa_mask_spec).  Key j is live for query row i of
+    batch b iff j < lengths[b % len(lengths)] (lengths given), j <= pos0 + i
+    (causal), |pos0 + i - j| <= window (window given)."""
+    sp = MxfaMaskSpec()
+    sp.flags = (MASK_CAUSAL if causal else 0) | (MASK_WINDOW if window is not None else 0) | \
+        (MASK_LENGTHS if lengths is not None else 0)
+    sp.window = int(window or 0)
+    sp.pos0 = int(pos0)
+    if lengths is not None:
+        arr = (ctypes.c_int32 * len(lengths))(*[int(x) for x in lengths])
+        sp.n_lengths = len(lengths)
+        sp.lengths = ctypes.cast(arr, ctypes.POINTER(ctypes.c_int32))
+        sp._keep = arr   # the array lives as long as the spec
+    return sp
+
+
 class MxfaError(RuntimeError):
     def __init__(self, status: int, detail: str):
         super().__init__(f"mxfa status {status} ({status_string(status)}): {detail}")
@@ -88,6 +120,11 @@ def _load():
     L.mxfa_set_rows_supports.restype = ctypes.c_int
     L.mxfa_set_rows.argtypes = [P, P, P, ctypes.c_void_p]
     L.mxfa_set_rows.restype = ctypes.c_int
+    L.mxfa_supports_masked.argtypes = [P, P, P, ctypes.POINTER(MxfaMaskSpec), ctypes.POINTER(MxfaParams), P]
+    L.mxfa_supports_masked.restype = ctypes.c_int
+    L.mxfa_flash_attn_ext_masked.argtypes = [P, P, P, ctypes.POINTER(MxfaMaskSpec), ctypes.POINTER(MxfaParams), P,
+                                             ctypes.c_void_p]
+    L.mxfa_flash_attn_ext_masked.restype = ctypes.c_int
     L.mxfa_release.argtypes = []
     L.mxfa_release.restype = None
     L.mxfa_status_string.argtypes = [ctypes.c_int]
@@ -206,6 +243,40 @@ def set_rows(dst: DeviceView, src: DeviceView, rows: DeviceView, stream: Optiona
         stream = torch.cuda.current_stream().cuda_stream
     dd, ds, dr = dst.desc(), src.desc(), rows.desc()
     rc = lib.mxfa_set_rows(ctypes.byref(dd), ctypes.byref(ds), ctypes.byref(dr), ctypes.c_void_p(int(stream)))
+    if rc != OK:
+        raise MxfaError(rc, last_error())
+    return dst
+
+
+def _out_view(q, v):
+    import torch
+
+    DV, Nh, Sq, B = int(v.ne[0]), int(q.ne[2]), int(q.ne[1]), int(q.ne[3])
+    out = torch.empty((B, Sq, Nh, DV), dtype=torch.float32, device="cuda")
+    return DeviceView(TYPE_F32, (DV, Nh, Sq, B), (4, 4 * DV, 4 * DV * Nh, 4 * DV * Nh * Sq), out.data_ptr(), out)
+
+
+def supports_masked(q, k, v, spec, scale, max_bias=0.0, logit_softcap=0.0, prec=PREC_F32, dst=None) -> bool:
+    """supports_op for a structured-mask call."""
+    keep, refs = _descs(q, k, v, None, dst)
+    p = make_params(scale, max_bias, logit_softcap, prec)
+    return bool(lib.mxfa_supports_masked(refs[0], refs[1], refs[2], ctypes.byref(spec), ctypes.byref(p), refs[4]))
+
+
+def flash_attn_ext_masked(q, k, v, spec, scale, max_bias=0.0, logit_softcap=0.0, prec=PREC_F32,
+                          dst: Optional[DeviceView] = None, stream: Optional[int] = None) -> DeviceView:
+    """flash_attn_ext with the mask given as metadata (`mask_spec(...)`):
+    the result equals flash_attn_ext with the equivalent dense F16 mask."""
+    import torch
+
+    if dst is None:
+        dst = _out_view(q, v)
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    keep, refs = _descs(q, k, v, None, dst)
+    p = make_params(scale, max_bias, logit_softcap, prec)
+    rc = lib.mxfa_flash_attn_ext_masked(refs[0], refs[1], refs[2], ctypes.byref(spec), ctypes.byref(p), refs[4],
+                                        ctypes.c_void_p(int(stream)))
     if rc != OK:
         raise MxfaError(rc, last_error())
     return dst

@@ -303,6 +303,56 @@ def c5(**kw) -> FaCase:
 BUILDERS = {"c1": c1, "c2": c2, "c3": c3, "c4s": c4_self, "c4x": c4_cross, "c5": c5}
 
 
+# -- structured masks ------------------------------------------------------------
+
+def structured_spec(case: FaCase) -> dict:
+    """The structured mask (keyword arguments of mxfa.mask_spec) that stands
+    for the dense mask the reference builds for this case: causal from the
+    query position (qwen3-lm.h:597-610), per-sequence lengths
+    (qwen3-lm.h:872-883, dit-sampler.h:296-309), the sliding window
+    (dit-sampler.h:262-289); {} for an unmasked case."""
+    m = case.meta
+    kind = m.get("kind")
+    if case.mask is None:
+        return {}
+    if kind == "lm_single":
+        return dict(causal=True, pos0=int(m["kv_pos"]))
+    if kind == "lm_batch":
+        return dict(lengths=[int(x) for x in m["lengths"]])
+    if kind == "dit_cross":
+        return dict(lengths=[int(m["enc_S"]) - int(p) for p in m["pads"]])
+    if kind == "dit_self" and m.get("window", 0) > 0 and m["S"] > m["window"]:
+        return dict(window=int(m["window"]))
+    raise ValueError(f"no structured form for case {case.name} ({kind})")
+
+
+def dense_mask_bits(spec: dict, Sq: int, Skv: int, B: int) -> np.ndarray:
+    """The dense F16 mask [B][1][Sq][Skv] (uint16 bits: 0 live, -inf dead)
+    that a structured mask (mask_spec keyword arguments) stands for."""
+    i = np.arange(Sq)[:, None] + int(spec.get("pos0", 0))
+    j = np.arange(Skv)[None, :]
+    lengths = spec.get("lengths")
+    out = np.empty((B, 1, Sq, Skv), dtype=np.uint16)
+    for b in range(B):
+        live = np.ones((Sq, Skv), dtype=bool)
+        if lengths is not None:
+            live &= j < lengths[b % len(lengths)]
+        if spec.get("causal"):
+            live &= j <= i
+        if spec.get("window") is not None:
+            live &= np.abs(i - j) <= spec["window"]
+        out[b, 0] = np.where(live, np.uint16(0), np.uint16(0xFC00))
+    return out
+
+
+def with_dense_mask(case: FaCase, spec: dict) -> FaCase:
+    """A copy of `case` whose mask is the dense form of `spec` ([Skv, Sq, 1, B])."""
+    Sq, Skv, B = int(case.q.ne[1]), int(case.k.ne[1]), int(case.q.ne[3])
+    bits = dense_mask_bits(spec, Sq, Skv, B).reshape(-1)
+    m = HostView(TYPE_F16, (Skv, Sq, 1, B), (2, 2 * Skv, 2 * Skv * Sq, 2 * Skv * Sq), bits)
+    return FaCase(case.name, case.q, case.k, case.v, m, case.scale, case.max_bias, case.softcap, dict(case.meta))
+
+
 # -- KV-cache write (GGML_OP_SET_ROWS) -------------------------------------------
 
 TYPE_I32, TYPE_I64 = 26, 27

@@ -18,7 +18,9 @@ heads, D=128, F32 Q, F16 K/V in a 2048-slot cache, F16 causal mask.  One
 
 The other configurations (C1, C3, C4 self/cross, C5) are reported under
 "configs" with their own bound (TFLOP/s vs MFMA peak, or KV GB/s vs the 8 TB/s
-HBM peak), and so are the KV-cache writes that precede C2 / C3 (GGML_OP_SET_ROWS:
+HBM peak), and so are the structured-mask variants c2m / c3m / c4xm (the
+same work with the mask given as metadata: mxfa_flash_attn_ext_masked) and
+the KV-cache writes that precede C2 / C3 (GGML_OP_SET_ROWS:
 kw2, kw3, and kw5 into a Q8_0 cache; GB/s of F32 read + converted row
 written + row ids, vs the HBM peak).  Inputs of bandwidth-bound configs are rotated over enough device
 copies that consecutive steps do not hit in the 256 MB Infinity Cache.
@@ -56,36 +58,48 @@ DESCR = {
     "c5": "Qwen3-4B decode over Q8_0 KV: B=4, 32/8 heads, D=128, KV 8192",
 }
 DESCR.update({
+    "c2m": "C2 with the causal mask as metadata (mxfa_flash_attn_ext_masked: no mask tensor, no classifier pass)",
+    "c3m": "C3 with the per-sequence lengths as metadata (splits sized from the live lengths)",
+    "c4xm": "C4 cross with the encoder padding as per-batch lengths (metadata)",
     "kw2": "KV-cache write (GGML_OP_SET_ROWS) of C2: 2048 tokens x 8 KV heads, F32 -> F16 cache [128, 2048, 8]",
     "kw3": "KV-cache write of C3: 1 token x 8 KV heads for each of 8 sets, F32 -> F16 4D cache view",
     "kw5": "KV-cache write of C2 into a Q8_0 cache: 2048 tokens x 8 KV heads, F32 -> Q8_0",
 })
-BOUND = {"c1": "hbm", "c2": "mfma", "c3": "hbm", "c4s": "mfma", "c4x": "hbm", "c5": "hbm"}
+BOUND = {"c1": "hbm", "c2": "mfma", "c3": "hbm", "c4s": "mfma", "c4x": "hbm", "c5": "hbm",
+         "c2m": "mfma", "c3m": "hbm", "c4xm": "hbm"}
 KERNEL = {"c1": "fa_decode", "c2": "fa_prefill", "c3": "fa_decode", "c4s": "fa_prefill", "c4x": "fa_prefill",
-          "c5": "fa_decode"}
+          "c5": "fa_decode", "c2m": "fa_prefill", "c3m": "fa_decode", "c4xm": "fa_prefill"}
+STRUCTURED = {"c2m": "c2", "c3m": "c3", "c4xm": "c4x"}   # structured-mask variant -> dense config
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def upload_copies(mx, case, n):
+def upload_copies(mx, case, n, with_mask=True):
     copies = []
     for _ in range(n):
         d = dict(q=mx.upload(case.q), k=mx.upload(case.k), v=mx.upload(case.v),
-                 m=mx.upload(case.mask) if case.mask is not None else None)
+                 m=mx.upload(case.mask) if (with_mask and case.mask is not None) else None)
         copies.append(d)
     return copies
 
 
-def time_case(mx, torch, case, steps, warmup, rotate_bytes=None):
-    """Returns (ms per call, per-kernel avg ms dict)."""
+def time_case(mx, torch, case, steps, warmup, rotate_bytes=None, spec=None):
+    """Returns (ms per call, per-kernel avg ms dict).  With `spec` (mask_spec
+    keyword arguments) the call is the structured-mask entry point and no
+    mask tensor exists; the algorithmic work is that of the dense case."""
     from mxfa import cases as C
 
     w = C.work(case)
+    if spec is not None:
+        w = dict(w)
+        w["bytes"] -= w["mask_bytes"]
+        w["mask_bytes"] = 0
+        spec_obj = mx.mask_spec(**spec)
     per_iter = w["bytes"]
     n_copies = 1 if rotate_bytes is None else int(min(16, max(1, math.ceil(rotate_bytes / max(per_iter, 1)))))
-    copies = upload_copies(mx, case, n_copies)
+    copies = upload_copies(mx, case, n_copies, with_mask=spec is None)
     outs = []
     for _ in range(n_copies):
         B, Sq, Nh, DV = case.out_shape
@@ -96,8 +110,12 @@ def time_case(mx, torch, case, steps, warmup, rotate_bytes=None):
 
     def step(i):
         c = copies[i % n_copies]
-        mx.flash_attn_ext(c["q"], c["k"], c["v"], c["m"], case.scale, case.max_bias, case.softcap,
-                          dst=outs[i % n_copies], stream=stream)
+        if spec is None:
+            mx.flash_attn_ext(c["q"], c["k"], c["v"], c["m"], case.scale, case.max_bias, case.softcap,
+                              dst=outs[i % n_copies], stream=stream)
+        else:
+            mx.flash_attn_ext_masked(c["q"], c["k"], c["v"], spec_obj, case.scale, case.max_bias, case.softcap,
+                                     dst=outs[i % n_copies], stream=stream)
 
     for i in range(warmup):
         step(i)
@@ -262,7 +280,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,kw2,kw3,kw5")
+    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c2m,c3m,c4xm,kw2,kw3,kw5")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB copy (counter calibration under rocprofv3)")
@@ -294,6 +312,15 @@ def main():
             case = C.SET_ROWS_BUILDERS[name]()
             ms, kms, w, ncp = time_set_rows(mxfa, torch, case, args.steps, args.warmup)
             results[name] = summarize_set_rows(name, ms, kms, w, ncp)
+            log(f"[bench] {name}: {json.dumps(results[name])}")
+            continue
+        spec = None
+        if name in STRUCTURED:
+            case = C.BUILDERS[STRUCTURED[name]]()
+            spec = C.structured_spec(case)
+            rot = ROTATE_BYTES if BOUND[name] == "hbm" else None
+            ms, kern, w, ncp = time_case(mxfa, torch, case, args.steps, args.warmup, rot, spec=spec)
+            results[name] = summarize(name, ms, kern, w, ncp)
             log(f"[bench] {name}: {json.dumps(results[name])}")
             continue
         case = C.BUILDERS[name]()

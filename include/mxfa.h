@@ -101,6 +101,43 @@ int mxfa_flash_attn_ext(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_t
                         const mxfa_tensor *mask, const mxfa_params *params, mxfa_tensor *dst,
                         void *hip_stream);
 
+/* Structured masks: GGML_OP_FLASH_ATTN_EXT with the mask given as metadata
+ * instead of an F16 tensor.  The reference builds every one of its masks on
+ * the host from a few integers and uploads O(Sq*Skv) F16 values per call:
+ * causal at src/qwen3-lm.h:597-610 and src/qwen3-enc.h:429-437, per-sequence
+ * lengths at src/qwen3-lm.h:872-883 and src/dit-sampler.h:296-309, and the
+ * sliding window at src/dit-sampler.h:262-289 and src/cond-enc.h:307-341.
+ * Key j is live for query row i (0 <= i < Sq) of batch b iff every flag set
+ * holds:
+ *   MXFA_MASK_LENGTHS  j < lengths[b % n_lengths]
+ *   MXFA_MASK_CAUSAL   j <= pos0 + i
+ *   MXFA_MASK_WINDOW   |pos0 + i - j| <= window
+ * mxfa_flash_attn_ext_masked(q, k, v, spec, ...) computes exactly what
+ * mxfa_flash_attn_ext(q, k, v, mask, ...) computes for the F16 mask
+ * [Skv, Sq, 1, B] holding 0 at live keys and -inf elsewhere (flags == 0:
+ * no mask).  Nothing is read from device memory for the mask: no mask
+ * upload, no mask reads, no mask-classifier pass, and the split-KV decode
+ * sizes its splits from the live lengths.  `lengths` is host memory read
+ * during the call (n_lengths is 1 or B, at most 64; values >= 0); pos0 >= 0,
+ * window >= 0, pos0 + Sq + window < 2^30. */
+#define MXFA_MASK_CAUSAL  1
+#define MXFA_MASK_WINDOW  2
+#define MXFA_MASK_LENGTHS 4
+
+typedef struct mxfa_mask_spec {
+    int32_t        flags;      /* MXFA_MASK_* bits */
+    int32_t        window;     /* MXFA_MASK_WINDOW */
+    int64_t        pos0;       /* absolute position of query row 0 (causal, window) */
+    int32_t        n_lengths;  /* MXFA_MASK_LENGTHS: entries of lengths[] */
+    const int32_t *lengths;    /* MXFA_MASK_LENGTHS: live key count per batch */
+} mxfa_mask_spec;
+
+int mxfa_supports_masked(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
+                         const mxfa_mask_spec *mask, const mxfa_params *params, const mxfa_tensor *dst);
+int mxfa_flash_attn_ext_masked(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
+                               const mxfa_mask_spec *mask, const mxfa_params *params, mxfa_tensor *dst,
+                               void *hip_stream);
+
 /* GGML_OP_SET_ROWS with an F32 source: the KV-cache write the reference
  * issues right before each attention node, ggml_set_rows(ctx, cache, rows_f32,
  * kv_rows) at src/qwen3-lm.h:453-454 ([D, S, Nkv] rows into the
