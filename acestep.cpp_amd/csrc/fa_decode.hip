@@ -235,17 +235,32 @@ __device__ __forceinline__ float ld_dev(const float *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Log-sum-exp merge of the n_splits partials of the tile's nr rows (run by
-// the last workgroup of the tile; partial row pr0 + r).  Phase A reads every
-// (row, split) (m, l) pair at once and turns them into weights in LDS;
-// phase B has each thread accumulate one dim of a few rows over all splits
-// with batches of independent loads (one memory round trip per batch).
+// Log-sum-exp merge of the ns partials of the tile's nr rows (run by the
+// last workgroup of the tile; partial row pr0 + r, partial slots a.n_splits
+// apart).  Thread -> dim t.tid % 128 of rows t.tid / 128 + 2j.  The O
+// partials of the first two rows of a thread (every row when nr <= 4, as in
+// decode) are loaded up front together with every (m, l) pair, so the merge
+// waits for one memory round trip; phase A turns (m, l) into weights in
+// LDS, phase B accumulates in split order (larger nr / ns load the rest in
+// batches of 16).
 constexpr int kMaxSplits = 64;
 __device__ void merge_splits(const FaArgs &a, const Tile &t, int64_t pr0, int nr, int ns, float *lds) {
-    const int stride = a.n_splits;            // partial slots per row
+    const int stride = a.n_splits;           // partial slots per row
     float *wm = lds;                         // [16][kMaxSplits]: m, then weights
     float *wl = wm + 16 * kMaxSplits;        // [16][kMaxSplits]: l
     float *Linv = wl + 16 * kMaxSplits;      // [16]
+    const int d = t.tid & (kD - 1);
+    const int rA = t.tid >> 7, rB = rA + 2;
+    float pa[16], pb[16];
+    {
+        const float *poA = a.part_o + (pr0 + rA) * stride * kD + d;
+        const float *poB = a.part_o + (pr0 + rB) * stride * kD + d;
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            pa[u] = (rA < nr && u < ns) ? ld_dev(poA + (int64_t)u * kD) : 0.0f;
+            pb[u] = (rB < nr && u < ns) ? ld_dev(poB + (int64_t)u * kD) : 0.0f;
+        }
+    }
     __syncthreads();                         // lds is free (waves' merge data consumed)
     for (int i0 = 0; i0 < nr * ns; i0 += 256 * 4) {
         float mv[4], lv[4];
@@ -282,15 +297,15 @@ __device__ void merge_splits(const FaArgs &a, const Tile &t, int64_t pr0, int nr
         Linv[r] = (Lt == 0.0f) ? 0.0f : 1.0f / Lt;
     }
     __syncthreads();
-    // phase B: thread -> dim t.tid % 128, rows t.tid / 128 + 2j
-    const int d = t.tid & (kD - 1);
-    for (int r = t.tid >> 7; r < nr; r += 2) {
+    // phase B: row r of this thread, the first 16 partials from `pre`
+    auto accum_row = [&](int r, const float (&pre)[16], bool have_pre) {
         const float *po = a.part_o + (pr0 + r) * stride * kD + d;
         float acc = 0.0f;
         for (int s0 = 0; s0 < ns; s0 += 16) {
             float ov[16];
 #pragma unroll
-            for (int u = 0; u < 16; u++) ov[u] = s0 + u < ns ? ld_dev(po + (int64_t)(s0 + u) * kD) : 0.0f;
+            for (int u = 0; u < 16; u++)
+                ov[u] = (s0 == 0 && have_pre) ? pre[u] : (s0 + u < ns ? ld_dev(po + (int64_t)(s0 + u) * kD) : 0.0f);
 #pragma unroll
             for (int u = 0; u < 16; u++)
                 if (s0 + u < ns) acc = fmaf(wm[r * kMaxSplits + s0 + u], ov[u], acc);
@@ -298,7 +313,10 @@ __device__ void merge_splits(const FaArgs &a, const Tile &t, int64_t pr0, int nr
         const int rg = t.rt * 16 + r;
         const int iq1o = rg / a.G, heado = t.kvh * a.G + rg % a.G;
         a.dst[(((int64_t)t.b * a.Sq + iq1o) * a.Nh + heado) * kD + d] = acc * Linv[r];
-    }
+    };
+    if (rA < nr) accum_row(rA, pa, true);
+    if (rB < nr) accum_row(rB, pb, true);
+    for (int r = rA + 4; r < nr; r += 2) accum_row(r, pa, false);
 }
 
 // Merges the 4 waves' (m, l, O^T) of the tile and writes the output (one
@@ -504,11 +522,12 @@ fa_decode_lds_kernel(const FaArgs a) {
         }
     };
 
-    // Speculative fill: the first stages of [k0, k1) go out before the
-    // live range is known.
+    // Speculative fill: the first stages of [k0, k1) -- the whole ring -- go
+    // out before the live range is known, so that the wait below (which the
+    // scan needs anyway) does not leave the ring empty behind it.
     const int kbw_spec = k0 + 16 * t.wave;
     const int nblk_spec = kbw_spec < k1 ? (k1 - kbw_spec + 63) / 64 : 0;
-    const int n_spec = min(NST - 1, nblk_spec);
+    const int n_spec = min(NST, nblk_spec);
     for (int s = 0; s < n_spec; s++) issue(kbw_spec + 64 * s, s);
 
     int lo = k0, hi = k1;
@@ -554,10 +573,7 @@ fa_decode_lds_kernel(const FaArgs a) {
         uint32_t dead = 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) dead |= (mk[i] == -INFINITY ? 1u : 0u) << i;
-        dead &= __shfl_xor(dead, 1);
-        dead &= __shfl_xor(dead, 2);
-        dead &= __shfl_xor(dead, 4);
-        dead &= __shfl_xor(dead, 8);
+        dead = and_rows16(dead);
 
         // S^T[key 4*g16 + i][row c16] = K . Q^T
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
@@ -580,8 +596,7 @@ fa_decode_lds_kernel(const FaArgs a) {
             xs[i] = xv;
             bmax = fmaxf(bmax, xv);
         }
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        bmax = max_half32(max_pair16(bmax));
         if (__any(bmax > m2 + 8.0f)) {
             const float mnew = fmaxf(m2, bmax);
             const float alpha = (mnew == -INFINITY) ? 1.0f : fast_exp2(m2 - mnew);
@@ -794,10 +809,7 @@ fa_decode_reg_kernel(const FaArgs a) {
         for (int sb = 0; sb < 2; sb++)
 #pragma unroll
             for (int i = 0; i < 4; i++) dead |= (mk[sb][i] == -INFINITY ? 1u : 0u) << (4 * sb + i);
-        dead &= __shfl_xor(dead, 1);
-        dead &= __shfl_xor(dead, 2);
-        dead &= __shfl_xor(dead, 4);
-        dead &= __shfl_xor(dead, 8);
+        dead = and_rows16(dead);
 
         // S^T tile: lane holds S^T[key 16sb+4g16+i][row c16]
         f32x4 s[2];
@@ -848,8 +860,7 @@ fa_decode_reg_kernel(const FaArgs a) {
                 xs[sb][i] = xv;
                 bmax = fmaxf(bmax, xv);
             }
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        bmax = max_half32(max_pair16(bmax));
         if (__any(bmax > m2 + 8.0f)) {
             const float mnew = fmaxf(m2, bmax);
             const float alpha = (mnew == -INFINITY) ? 1.0f : fast_exp2(m2 - mnew);

@@ -74,6 +74,35 @@ struct FaArgs {
     int32_t sm_len[kSmMaxLen];
 };
 
+// Cross-lane steps at VALU latency (DPP, v_permlane*_swap) instead of LDS
+// crossbar permutes (ds_bpermute, ~100 cycles each).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+// AND over the 16 lanes of each row: quad_perm [1,0,3,2] and [2,3,0,1]
+// combine each quad, row_half_mirror (i <- 7-i) the two quads of each 8,
+// row_mirror (i <- 15-i) the two 8s.  Needs every lane active.
+__device__ __forceinline__ uint32_t and_rows16(uint32_t v) {
+    v &= dpp_u32<0xB1>(v);
+    v &= dpp_u32<0x4E>(v);
+    v &= dpp_u32<0x141>(v);
+    v &= dpp_u32<0x140>(v);
+    return v;
+}
+// max of x over lanes l and l ^ 16 (v_permlane16_swap pairs rows r, r ^ 1)
+// and over lanes l and l ^ 32 (v_permlane32_swap pairs the two halves)
+__device__ __forceinline__ float max_pair16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                    false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float max_half32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                    false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+
 // Live keys [lo, hi) of query row iq1 of batch b under the structured mask
 // (both ends are non-decreasing in iq1, so the rows of a tile cover
 // [lo(first row), hi(last row)) and all of them see [lo(last), hi(first))).
