@@ -380,6 +380,17 @@ int ensure_workspace(size_t bytes, int64_t n_tickets, hipStream_t stream, void *
     std::lock_guard<std::mutex> lock(g_ws_mu);
     if ((size_t)dev >= g_ws.size()) g_ws.resize(dev + 1);
     Workspace &ws = g_ws[dev];
+    if (ws.size < bytes || ws.n_tickets < n_tickets) {
+        // Growing allocates and synchronises, which a stream under HIP graph
+        // capture cannot do: the first call of a shape must run eagerly (or
+        // through mxfa_reserve) before a graph containing it is captured.
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return fail(MXFA_ERR_UNSUPPORTED,
+                        "workspace must grow (%zu bytes, %lld tickets) while the stream is being captured; "
+                        "run the call once eagerly or call mxfa_reserve() before capture",
+                        bytes, (long long)n_tickets);
+    }
     if (ws.size < bytes) {
         if (ws.ptr) {
             // queued kernels may still read the old buffer
@@ -552,6 +563,17 @@ int mxfa_flash_attn_ext(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_t
     const int rc = check(q, k, v, mask, params, dst);
     if (rc != MXFA_OK) return rc;
     return run(q, k, v, mask, params, dst, hip_stream, nullptr);
+}
+
+int mxfa_reserve(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
+                 const mxfa_params *params, void *hip_stream) {
+    const int rc = check(q, k, v, mask, params, nullptr);
+    if (rc != MXFA_OK) return rc;
+    Plan pl;
+    make_plan(q, k, v, mask, params, nullptr, pl);
+    void *ws = nullptr;
+    int *tickets = nullptr;
+    return ensure_workspace(pl.ws_bytes, pl.n_tickets, (hipStream_t)hip_stream, &ws, &tickets);
 }
 
 int mxfa_supports_masked(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_mask_spec *mask,

@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "mxfa_flash_attn_ext",
     "mxfa_supports_masked",
     "mxfa_flash_attn_ext_masked",
+    "mxfa_reserve",
     "mxfa_set_rows_supports",
     "mxfa_set_rows",
     "mxfa_release",
@@ -116,6 +117,8 @@ def _load():
     L.mxfa_supports.restype = ctypes.c_int
     L.mxfa_flash_attn_ext.argtypes = [P, P, P, P, ctypes.POINTER(MxfaParams), P, ctypes.c_void_p]
     L.mxfa_flash_attn_ext.restype = ctypes.c_int
+    L.mxfa_reserve.argtypes = [P, P, P, P, ctypes.POINTER(MxfaParams), ctypes.c_void_p]
+    L.mxfa_reserve.restype = ctypes.c_int
     L.mxfa_set_rows_supports.argtypes = [P, P, P]
     L.mxfa_set_rows_supports.restype = ctypes.c_int
     L.mxfa_set_rows.argtypes = [P, P, P, ctypes.c_void_p]
@@ -222,6 +225,20 @@ def flash_attn_ext(q, k, v, mask, scale, max_bias=0.0, logit_softcap=0.0, prec=P
     if rc != OK:
         raise MxfaError(rc, last_error())
     return dst
+
+
+def reserve(q, k, v, mask, scale, max_bias=0.0, logit_softcap=0.0, prec=PREC_F32, stream=None) -> None:
+    """Grows the engine's workspace for this call's shapes without launching
+    anything, so that the call can then be captured into a HIP graph."""
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    keep, refs = _descs(q, k, v, mask, None)
+    p = make_params(scale, max_bias, logit_softcap, prec)
+    rc = lib.mxfa_reserve(refs[0], refs[1], refs[2], refs[3], ctypes.byref(p), ctypes.c_void_p(int(stream)))
+    if rc != OK:
+        raise MxfaError(rc, last_error())
 
 
 def set_rows_supports(dst, src, rows) -> bool:

@@ -61,6 +61,7 @@ DESCR.update({
     "c2m": "C2 with the causal mask as metadata (mxfa_flash_attn_ext_masked: no mask tensor, no classifier pass)",
     "c3m": "C3 with the per-sequence lengths as metadata (splits sized from the live lengths)",
     "c4xm": "C4 cross with the encoder padding as per-batch lengths (metadata)",
+    "dstep": "Qwen3-0.6B decode token: 28 layers x (KV write of K and V + FA over a 512-key window), eager vs HIP graph replay",
     "kw2": "KV-cache write (GGML_OP_SET_ROWS) of C2: 2048 tokens x 8 KV heads, F32 -> F16 cache [128, 2048, 8]",
     "kw3": "KV-cache write of C3: 1 token x 8 KV heads for each of 8 sets, F32 -> F16 4D cache view",
     "kw5": "KV-cache write of C2 into a Q8_0 cache: 2048 tokens x 8 KV heads, F32 -> Q8_0",
@@ -182,6 +183,83 @@ def time_set_rows(mx, torch, case, steps, warmup, rotate_bytes=ROTATE_BYTES):
     return ms, (tot / n if n else None), w, n_copies
 
 
+def time_decode_step(mx, torch, steps, warmup, L=28, Nh=16, Nkv=8, max_seq=8192, W=512, pos=511):
+    """One decode token of a Qwen3-0.6B-shaped LM through the engine: per
+    layer the KV-cache write of K and V (set_rows, src/qwen3-lm.h:453-454)
+    and attention over the 512-key window with its causal mask
+    (:465-469).  Timed eagerly (the host issues 3 * L calls per token) and
+    as one HIP graph replay per token (the reference's static decode graph,
+    src/static-graph.h)."""
+    Dh = 128
+    dev = "cuda"
+    cache_k = [torch.zeros(Nkv, max_seq, Dh, dtype=torch.float16, device=dev) for _ in range(L)]
+    cache_v = [torch.zeros(Nkv, max_seq, Dh, dtype=torch.float16, device=dev) for _ in range(L)]
+    for t_ in cache_k + cache_v:
+        t_[:, :pos].normal_()
+    k_new = [torch.randn(Nkv, 1, Dh, device=dev) for _ in range(L)]
+    v_new = [torch.randn(Nkv, 1, Dh, device=dev) for _ in range(L)]
+    qs = [torch.randn(Nh, 1, Dh, device=dev) for _ in range(L)]
+    outs = [torch.empty(1, 1, Nh, Dh, device=dev) for _ in range(L)]
+    rows = torch.full((1,), pos, dtype=torch.int64, device=dev)
+    j = torch.arange(W, device=dev)
+    mask = torch.where(j <= pos, 0.0, float("-inf")).half().view(1, W)
+    cnb = (2, 2 * Dh, 2 * Dh * max_seq, 2 * Dh * max_seq * Nkv)
+    views = []
+    for l in range(L):
+        views.append((
+            mx.DeviceView(1, (Dh, max_seq, Nkv, 1), cnb, cache_k[l].data_ptr(), cache_k[l]),
+            mx.DeviceView(1, (Dh, max_seq, Nkv, 1), cnb, cache_v[l].data_ptr(), cache_v[l]),
+            mx.DeviceView(1, (Dh, W, Nkv, 1), cnb, cache_k[l].data_ptr(), cache_k[l]),
+            mx.DeviceView(1, (Dh, W, Nkv, 1), cnb, cache_v[l].data_ptr(), cache_v[l]),
+            mx.DeviceView(0, (Dh, 1, Nkv, 1), (4, 4 * Dh, 4 * Dh, 4 * Dh * Nkv), k_new[l].data_ptr(), k_new[l]),
+            mx.DeviceView(0, (Dh, 1, Nkv, 1), (4, 4 * Dh, 4 * Dh, 4 * Dh * Nkv), v_new[l].data_ptr(), v_new[l]),
+            mx.DeviceView(0, (Dh, 1, Nh, 1), (4, 4 * Dh, 4 * Dh, 4 * Dh * Nh), qs[l].data_ptr(), qs[l]),
+            mx.DeviceView(0, (Dh, Nh, 1, 1), (4, 4 * Dh, 4 * Dh * Nh, 4 * Dh * Nh), outs[l].data_ptr(), outs[l])))
+    dr = mx.DeviceView(27, (1, 1, 1, 1), (8, 8, 8, 8), rows.data_ptr(), rows)
+    dm = mx.DeviceView(1, (W, 1, 1, 1), (2, 2 * W, 2 * W, 2 * W), mask.data_ptr(), mask)
+    scale = 1.0 / math.sqrt(Dh)
+
+    def step(stream):
+        for kc, vc, kw, vw, ks, vs, q, o in views:
+            mx.set_rows(kc, ks, dr, stream=stream)
+            mx.set_rows(vc, vs, dr, stream=stream)
+            mx.flash_attn_ext(q, kw, vw, dm, scale, dst=o, stream=stream)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    cur = torch.cuda.current_stream().cuda_stream
+    eager_ms = timed(lambda: step(cur))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            step(s.cuda_stream)
+    torch.cuda.synchronize()
+    graph_ms = timed(g.replay)
+    # per-kernel device time of one token (HIP events on the launch stream)
+    mx.timing_reset()
+    mx.timing_enable(True)
+    step(cur)
+    torch.cuda.synchronize()
+    mx.timing_enable(False)
+    dev_ms = sum(mx.timing_read(f)[0] for f in ("set_rows", "fa_decode"))
+    mx.timing_reset()
+    return dict(workload=DESCR["dstep"], layers=L, launches_per_token=3 * L, eager_us=round(eager_ms * 1e3, 2),
+                graph_us=round(graph_ms * 1e3, 2), speedup=round(eager_ms / graph_ms, 3),
+                kernel_sum_us=round(dev_ms * 1e3, 2))
+
+
 def summarize_set_rows(name, ms, kms, w, n_copies):
     out = dict(workload=DESCR[name], ms=round(ms, 5), bytes=w["bytes"], rows=w["rows"], copies=n_copies,
                bound="hbm")
@@ -280,7 +358,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c2m,c3m,c4xm,kw2,kw3,kw5")
+    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c2m,c3m,c4xm,kw2,kw3,kw5,dstep")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB copy (counter calibration under rocprofv3)")
@@ -312,6 +390,10 @@ def main():
             case = C.SET_ROWS_BUILDERS[name]()
             ms, kms, w, ncp = time_set_rows(mxfa, torch, case, args.steps, args.warmup)
             results[name] = summarize_set_rows(name, ms, kms, w, ncp)
+            log(f"[bench] {name}: {json.dumps(results[name])}")
+            continue
+        if name == "dstep":
+            results[name] = time_decode_step(mxfa, torch, max(20, args.steps // 4), 5)
             log(f"[bench] {name}: {json.dumps(results[name])}")
             continue
         spec = None

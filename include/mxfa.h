@@ -165,6 +165,25 @@ int mxfa_flash_attn_ext_masked(const mxfa_tensor *q, const mxfa_tensor *k, const
 int mxfa_set_rows_supports(const mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_tensor *rows);
 int mxfa_set_rows(mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_tensor *rows, void *hip_stream);
 
+/* HIP graph capture / replay.  The reference replays its static decode
+ * graph (src/static-graph.h, src/graph-arena.h, src/qwen3-lm.h:36-58): the
+ * node arguments stay at fixed addresses and only their contents change
+ * between replays (kv_rows, masks, positions).  Every mxfa entry point is
+ * capture-safe -- kernels only, no memset, no host synchronisation, split
+ * tickets reset by the kernels themselves -- except when the per-device
+ * workspace has to grow: that call fails with MXFA_ERR_UNSUPPORTED while
+ * `hip_stream` is being captured.  mxfa_reserve() grows the workspace for
+ * the given FA call on the current device (synchronising `hip_stream` if it
+ * replaces a buffer) without launching anything; so does any eager call of
+ * the same shapes.  Replays reuse the workspace and must not overlap in
+ * time with other mxfa calls on the device.  A structured mask's host-side
+ * values (pos0, window, lengths) are captured with the launch: for values
+ * that change between replays use the dense mask, which lives in device
+ * memory like the reference's.  (No counterpart in ggml: a backend calls
+ * mxfa_reserve from its graph set-up.) */
+int mxfa_reserve(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
+                 const mxfa_params *params, void *hip_stream);
+
 /* Free the workspaces of every device (synchronises each device first). */
 void mxfa_release(void);
 

@@ -1,0 +1,175 @@
+"""GPU: HIP graph capture and replay of a decode step (the reference's static
+decode graph: src/static-graph.h, src/qwen3-lm.h:36-58, and the per-layer
+KV write + attention of :448-469).
+
+A step of L layers -- KV-cache write of K and V (mxfa_set_rows), then
+attention over the cache window (mxfa_flash_attn_ext with the causal mask) --
+is captured once into a graph (torch.cuda.graph over the engine's stream)
+and replayed for several tokens.  Between replays the host rewrites the
+static inputs in place (new rows, row id, mask, queries), as the reference
+does, and runs eager work on the device.  Every replay's outputs and caches
+must equal, bit for bit, an eager twin that runs the same calls on its own
+copy of the state.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+D = 128
+
+
+@pytest.fixture(scope="module")
+def mx():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import mxfa
+
+    return mxfa
+
+
+class Step:
+    """Static buffers of one decode step (fixed addresses, as in a graph)."""
+
+    def __init__(self, mx, L, Nh, Nkv, max_seq, n_kv_pad, seed):
+        import torch
+
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        self.mx, self.L, self.Nh, self.Nkv, self.max_seq, self.n_kv_pad = mx, L, Nh, Nkv, max_seq, n_kv_pad
+        dev = "cuda"
+        self.cache_k = [(torch.randn(Nkv, max_seq, D, generator=g) * 0.5).half().to(dev) for _ in range(L)]
+        self.cache_v = [(torch.randn(Nkv, max_seq, D, generator=g) * 0.5).half().to(dev) for _ in range(L)]
+        self.k_new = [torch.zeros(Nkv, 1, D, device=dev) for _ in range(L)]
+        self.v_new = [torch.zeros(Nkv, 1, D, device=dev) for _ in range(L)]
+        self.q = [torch.zeros(Nh, 1, D, device=dev) for _ in range(L)]
+        self.rows = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.mask = torch.zeros(1, n_kv_pad, dtype=torch.float16, device=dev)
+        self.out = [torch.zeros(1, 1, Nh, D, device=dev) for _ in range(L)]
+
+    def views(self, l):
+        mx, Nh, Nkv, ms, W = self.mx, self.Nh, self.Nkv, self.max_seq, self.n_kv_pad
+        kc, vc = self.cache_k[l], self.cache_v[l]
+        cache_nb = (2, 2 * D, 2 * D * ms, 2 * D * ms * Nkv)
+        dk = mx.DeviceView(1, (D, ms, Nkv, 1), cache_nb, kc.data_ptr(), kc)
+        dv = mx.DeviceView(1, (D, ms, Nkv, 1), cache_nb, vc.data_ptr(), vc)
+        kwin = mx.DeviceView(1, (D, W, Nkv, 1), cache_nb, kc.data_ptr(), kc)
+        vwin = mx.DeviceView(1, (D, W, Nkv, 1), cache_nb, vc.data_ptr(), vc)
+        src_nb = (4, 4 * D, 4 * D, 4 * D * Nkv)
+        ks = mx.DeviceView(0, (D, 1, Nkv, 1), src_nb, self.k_new[l].data_ptr(), self.k_new[l])
+        vs = mx.DeviceView(0, (D, 1, Nkv, 1), src_nb, self.v_new[l].data_ptr(), self.v_new[l])
+        rows = mx.DeviceView(27, (1, 1, 1, 1), (8, 8, 8, 8), self.rows.data_ptr(), self.rows)
+        q = mx.DeviceView(0, (D, 1, Nh, 1), (4, 4 * D, 4 * D, 4 * D * Nh), self.q[l].data_ptr(), self.q[l])
+        m = mx.DeviceView(1, (W, 1, 1, 1), (2, 2 * W, 2 * W, 2 * W), self.mask.data_ptr(), self.mask)
+        o = mx.DeviceView(0, (D, Nh, 1, 1), (4, 4 * D, 4 * D * Nh, 4 * D * Nh), self.out[l].data_ptr(),
+                          self.out[l])
+        return dk, dv, kwin, vwin, ks, vs, rows, q, m, o
+
+    def run(self, stream=None):
+        """The step's launches, in the reference's order."""
+        for l in range(self.L):
+            dk, dv, kwin, vwin, ks, vs, rows, q, m, o = self.views(l)
+            self.mx.set_rows(dk, ks, rows, stream=stream)
+            self.mx.set_rows(dv, vs, rows, stream=stream)
+            self.mx.flash_attn_ext(q, kwin, vwin, m, 1.0 / D ** 0.5, dst=o, stream=stream)
+
+    def set_inputs(self, pos, seed):
+        """Host-side input update of one token (in place, fixed addresses)."""
+        import torch
+
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        for l in range(self.L):
+            self.k_new[l].copy_(torch.randn(self.Nkv, 1, D, generator=g))
+            self.v_new[l].copy_(torch.randn(self.Nkv, 1, D, generator=g))
+            self.q[l].copy_(torch.randn(self.Nh, 1, D, generator=g))
+        self.rows.fill_(pos)
+        j = torch.arange(self.n_kv_pad)
+        self.mask.copy_(torch.where(j <= pos, 0.0, float("-inf")).half().view(1, -1))
+
+
+def test_decode_step_graph_replays_match_eager(mx):
+    import torch
+
+    L, Nh, Nkv, max_seq, W = 4, 16, 8, 1024, 512
+    graph_state = Step(mx, L, Nh, Nkv, max_seq, W, seed=1)
+    eager_state = Step(mx, L, Nh, Nkv, max_seq, W, seed=1)
+    base = 300
+    # eager warm-up of the graph's own buffers sizes the engine's workspace
+    graph_state.set_inputs(base - 1, seed=99)
+    graph_state.run()
+    eager_state.set_inputs(base - 1, seed=99)
+    eager_state.run()
+    torch.cuda.synchronize()
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            graph_state.run(stream=s.cuda_stream)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+
+    for step in range(4):
+        pos = base + step
+        print(f"[graph] replay {step} at position {pos}", flush=True)
+        graph_state.set_inputs(pos, seed=step)
+        eager_state.set_inputs(pos, seed=step)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        eager_state.run()                    # eager work between replays
+        _ = torch.randn(1 << 20, device="cuda").sum()
+        torch.cuda.synchronize()
+        for l in range(L):
+            assert torch.equal(graph_state.out[l], eager_state.out[l]), (step, l)
+            assert torch.equal(graph_state.cache_k[l], eager_state.cache_k[l]), (step, l)
+            assert torch.equal(graph_state.cache_v[l], eager_state.cache_v[l]), (step, l)
+        # the new token's rows were written, and attention saw them
+        assert float(graph_state.out[0].abs().sum()) > 0
+
+
+def test_growth_under_capture_is_refused(mx):
+    """A call whose workspace would have to grow while the stream is being
+    captured fails cleanly (no allocation, nothing launched); after
+    mxfa_reserve the same call captures and replays."""
+    import torch
+
+    from mxfa import cases as C
+
+    c = C.lm_batch("t", N=8, Nh=32, Nkv=8, max_seq=8192, lmin=6000, lmax=8192)   # a large split workspace
+    mx.release()
+    dq, dk, dv, dm = mx.upload(c.q), mx.upload(c.k), mx.upload(c.v), mx.upload(c.mask)
+    B, Sq, Nh, DV = c.out_shape
+    out = torch.zeros(B, Sq, Nh, DV, device="cuda")
+    dst = mx.DeviceView(0, (DV, Nh, Sq, B), (4, 4 * DV, 4 * DV * Nh, 4 * DV * Nh * Sq), out.data_ptr(), out)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    raised = None
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            try:
+                mx.flash_attn_ext(dq, dk, dv, dm, c.scale, dst=dst, stream=s.cuda_stream)
+            except mx.MxfaError as e:
+                raised = e
+    torch.cuda.synchronize()
+    assert raised is not None and raised.status == mx.ERR_UNSUPPORTED, raised
+    assert "captured" in raised.detail
+    mx.reserve(dq, dk, dv, dm, c.scale)
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g2, stream=s):
+            mx.flash_attn_ext(dq, dk, dv, dm, c.scale, dst=dst, stream=s.cuda_stream)
+    torch.cuda.synchronize()
+    ref = torch.zeros_like(out)
+    refv = mx.DeviceView(0, dst.ne, dst.nb, ref.data_ptr(), ref)
+    for _ in range(3):
+        out.zero_()
+        g2.replay()
+        torch.cuda.synchronize()
+        mx.flash_attn_ext(dq, dk, dv, dm, c.scale, dst=refv)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
