@@ -134,9 +134,21 @@ __device__ __forceinline__ const float *q_row(const FaArgs &a, const Tile &t) {
 }
 
 // Q^T operand of the 16x16x32 MFMA: lane holds Q[row][32s + 8*g16 + e],
-// converted like ggml converts Q to K's vec-dot type (round to nearest even).
+// converted like ggml converts Q to K's vec-dot type (round to nearest even),
+// or loaded as it is when Q is already stored in that type (a.q16).
 template <int T>
 __device__ __forceinline__ void load_q16(const FaArgs &a, const Tile &t, typename Mfma16<T>::v8 (&qb)[4]) {
+    if (a.q16) {
+        const uint16_t *qh = (const uint16_t *)(a.q + (int64_t)t.iq1 * a.q_nb1 + (int64_t)t.head * a.q_nb2 +
+                                                (int64_t)t.b * a.q_nb3);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            u16x8 x = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (t.row_ok) x = *(const u16x8 *)(qh + 32 * s + 8 * t.g16);
+            qb[s] = __builtin_bit_cast(typename Mfma16<T>::v8, x);
+        }
+        return;
+    }
     const float *qp = q_row(a, t);
 #pragma unroll
     for (int s = 0; s < 4; s++) {

@@ -344,19 +344,31 @@ fa_prefill_kernel(const FaArgs a) {
     int kt = next_live(0);
     if (kt < n_kt) issue(kt, std::integral_constant<int, 0>{});
 
-    // Q^T operand for the 8 dim-steps of 16: Q[qrow][16t + 8h + e].
+    // Q^T operand for the 8 dim-steps of 16: Q[qrow][16t + 8h + e], F32
+    // rounded to T (round to nearest even, as ggml converts Q to K's
+    // vec-dot type), or already stored in T (a.q16).
     V8 qb[8];
     {
-        const float *qp = (const float *)(a.q + (int64_t)qrow_c * a.q_nb1 + (int64_t)head * a.q_nb2 +
-                                          (int64_t)b * a.q_nb3);
+        const char *qrow_p = a.q + (int64_t)qrow_c * a.q_nb1 + (int64_t)head * a.q_nb2 + (int64_t)b * a.q_nb3;
+        if (a.q16) {
+            const uint16_t *qh = (const uint16_t *)qrow_p;
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-            f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
-            if (row_ok) {
-                x0 = *(const f32x4 *)(qp + 16 * t + 8 * h);
-                x1 = *(const f32x4 *)(qp + 16 * t + 8 * h + 4);
+            for (int t = 0; t < 8; t++) {
+                u16x8 x = {0, 0, 0, 0, 0, 0, 0, 0};
+                if (row_ok) x = *(const u16x8 *)(qh + 16 * t + 8 * h);
+                qb[t] = __builtin_bit_cast(V8, x);
             }
-            qb[t] = __builtin_bit_cast(V8, cvt8<T>(x0, x1));
+        } else {
+            const float *qp = (const float *)qrow_p;
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
+                if (row_ok) {
+                    x0 = *(const f32x4 *)(qp + 16 * t + 8 * h);
+                    x1 = *(const f32x4 *)(qp + 16 * t + 8 * h + 4);
+                }
+                qb[t] = __builtin_bit_cast(V8, cvt8<T>(x0, x1));
+            }
         }
     }
 

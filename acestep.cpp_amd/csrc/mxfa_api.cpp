@@ -153,6 +153,102 @@ int check_set_rows(const mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_te
     return MXFA_OK;
 }
 
+// Validation of a pre-attention fusion call; fills `a` (and *out_type).
+int check_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *qw,
+                    const mxfa_tensor *kw, const mxfa_tensor *pos, const mxfa_norm_rope_params *p,
+                    const mxfa_tensor *qo, const mxfa_tensor *ko, const mxfa_tensor *vo, const mxfa_tensor *rows,
+                    NormRopeArgs *a, int *out_type) {
+    if (!q || !k || !v || !qw || !kw || !pos || !p || !qo || !ko || !vo)
+        return fail(MXFA_ERR_INVALID, "q, k, v, norms, positions, params and outputs are required");
+    for (const mxfa_tensor *t : {q, k, v, qw, kw, pos, qo, ko, vo, rows}) {
+        if (!t) continue;
+        for (int i = 0; i < 4; i++)
+            if (t->ne[i] <= 0) return fail(MXFA_ERR_INVALID, "ne[%d] = %lld must be positive", i, (long long)t->ne[i]);
+        if (!t->data) return fail(MXFA_ERR_INVALID, "NULL data pointer");
+    }
+    for (const mxfa_tensor *t : {q, k, v})
+        if (t->type != MXFA_TYPE_F32 || t->ne[0] != kD || t->nb[0] != 4 || !is_aligned(t->data, 16) ||
+            t->nb[1] % 16 || t->nb[2] % 16 || t->nb[3] % 16)
+            return fail(MXFA_ERR_UNSUPPORTED, "q/k/v must be F32 rows of 128 values, 16-byte aligned");
+    const int64_t Nh = q->ne[1], Nkv = k->ne[1], S = q->ne[2], B = q->ne[3];
+    if (v->ne[1] != Nkv || k->ne[2] != S || v->ne[2] != S || k->ne[3] != B || v->ne[3] != B)
+        return fail(MXFA_ERR_INVALID, "q/k/v shapes disagree");
+    for (const mxfa_tensor *t : {qw, kw})
+        if (t->type != MXFA_TYPE_F32 || t->ne[0] != kD || t->ne[1] * t->ne[2] * t->ne[3] != 1 || t->nb[0] != 4)
+            return fail(MXFA_ERR_INVALID, "norm weights must be F32 [128]");
+    for (const mxfa_tensor *t : {qw, kw})
+        if (!is_aligned(t->data, 16)) return fail(MXFA_ERR_UNSUPPORTED, "norm weights must be 16-byte aligned");
+    if (pos->type != MXFA_TYPE_I32 || pos->ne[0] != S || (pos->ne[1] != 1 && pos->ne[1] != B) || pos->ne[2] != 1 ||
+        pos->ne[3] != 1 || pos->nb[0] != 4 || (pos->ne[1] > 1 && pos->nb[1] != 4 * (size_t)S) ||
+        !is_aligned(pos->data, 4))
+        return fail(MXFA_ERR_INVALID, "positions must be I32 [S] or [S, B], contiguous");
+    const int ot = qo->type;
+    if (ot != MXFA_TYPE_F16 && ot != MXFA_TYPE_BF16)
+        return fail(MXFA_ERR_UNSUPPORTED, "outputs must be F16 or BF16 (type %d)", ot);
+    if (qo->ne[0] != kD || qo->ne[1] != Nh || qo->ne[2] != S || qo->ne[3] != B || qo->nb[0] != 2 ||
+        qo->nb[1] != 2 * (size_t)kD || qo->nb[2] != qo->nb[1] * Nh || qo->nb[3] != qo->nb[2] * S ||
+        !is_aligned(qo->data, 8))
+        return fail(MXFA_ERR_INVALID, "q_out must be contiguous [128, Nh, S, B]");
+    for (const mxfa_tensor *t : {ko, vo})
+        if (t->type != ot || t->ne[0] != kD || t->ne[2] != Nkv || t->ne[3] != B || t->nb[0] != 2 ||
+            !is_aligned(t->data, 8) || t->nb[1] % 8 || t->nb[2] % 8 || t->nb[3] % 8)
+            return fail(MXFA_ERR_INVALID, "k_out/v_out must be [128, M, Nkv, B] of q_out's type, 8-byte aligned rows");
+    if (ko->ne[1] != vo->ne[1] || ko->nb[1] != vo->nb[1] || ko->nb[2] != vo->nb[2] || ko->nb[3] != vo->nb[3])
+        return fail(MXFA_ERR_INVALID, "k_out and v_out layouts differ");
+    if (rows) {
+        const size_t es = rows->type == MXFA_TYPE_I64 ? 8 : 4;
+        if ((rows->type != MXFA_TYPE_I64 && rows->type != MXFA_TYPE_I32) || rows->ne[0] != S || B % rows->ne[1] ||
+            rows->ne[2] != 1 || rows->ne[3] != 1 || rows->nb[0] != es || !is_aligned(rows->data, es) ||
+            rows->nb[1] % es)
+            return fail(MXFA_ERR_INVALID, "rows must be I64/I32 [S, R] with B %% R == 0");
+    } else if (ko->ne[1] < S) {
+        return fail(MXFA_ERR_INVALID, "without rows, k_out/v_out need at least S rows");
+    }
+    if (!(p->eps >= 0.0f) || !std::isfinite(p->eps) || !(p->freq_base > 0.0f) || !std::isfinite(p->freq_base))
+        return fail(MXFA_ERR_INVALID, "eps / freq_base invalid");
+    if ((Nh + 2 * Nkv) * S * B >= ((int64_t)1 << 40) || S * B >= ((int64_t)1 << 31) || Nh + 2 * Nkv > 4096)
+        return fail(MXFA_ERR_UNSUPPORTED, "too many rows");
+    if (a) {
+        NormRopeArgs &r = *a;
+        r = NormRopeArgs{};
+        r.q = (const char *)q->data;
+        r.k = (const char *)k->data;
+        r.v = (const char *)v->data;
+        for (int i = 0; i < 3; i++) {
+            r.q_nb[i] = (int64_t)q->nb[i + 1];
+            r.k_nb[i] = (int64_t)k->nb[i + 1];
+            r.v_nb[i] = (int64_t)v->nb[i + 1];
+        }
+        r.q_w = (const float *)qw->data;
+        r.k_w = (const float *)kw->data;
+        r.pos = (const int32_t *)pos->data;
+        r.pos_per_batch = pos->ne[1] > 1;
+        r.eps = p->eps;
+        r.theta_scale = std::pow(p->freq_base, -2.0f / (float)kD);
+        r.clamp_v = p->clamp_v != 0;
+        r.q_out = (char *)qo->data;
+        r.k_out = (char *)ko->data;
+        r.v_out = (char *)vo->data;
+        r.kv_nb1 = (int64_t)ko->nb[1];
+        r.kv_nb2 = (int64_t)ko->nb[2];
+        r.kv_nb3 = (int64_t)ko->nb[3];
+        r.kv_rows = ko->ne[1];
+        if (rows) {
+            r.rows = (const char *)rows->data;
+            r.r_nb0 = (int64_t)rows->nb[0];
+            r.r_nb1 = (int64_t)rows->nb[1];
+            r.r_ne1 = (int32_t)rows->ne[1];
+            r.rows_i64 = rows->type == MXFA_TYPE_I64;
+        }
+        r.Nh = (int32_t)Nh;
+        r.Nkv = (int32_t)Nkv;
+        r.S = (int32_t)S;
+        r.B = (int32_t)B;
+    }
+    if (out_type) *out_type = ot;
+    return MXFA_OK;
+}
+
 struct Plan {
     bool prefill = false;
     FaArgs args{};
@@ -172,7 +268,12 @@ int check(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, cons
         for (int i = 0; i < 4; i++)
             if (t->ne[i] <= 0) return fail(MXFA_ERR_INVALID, "ne[%d] = %lld must be positive", i, (long long)t->ne[i]);
     }
-    if (q->type != MXFA_TYPE_F32) return fail(MXFA_ERR_UNSUPPORTED, "q must be F32 (type %d)", q->type);
+    // Q is F32 (ggml's FA input), or already in K's 16-bit type (F16 / BF16
+    // K; the fused pre-attention kernel writes it so): ggml converts Q to
+    // K's type before the KQ product, so both give the same operands.
+    const bool q16 = (q->type == MXFA_TYPE_F16 || q->type == MXFA_TYPE_BF16) && q->type == k->type;
+    if (q->type != MXFA_TYPE_F32 && !q16)
+        return fail(MXFA_ERR_UNSUPPORTED, "q must be F32 or K's 16-bit type (q type %d, k type %d)", q->type, k->type);
     if (k->type != MXFA_TYPE_F16 && k->type != MXFA_TYPE_BF16 && k->type != MXFA_TYPE_Q8_0)
         return fail(MXFA_ERR_UNSUPPORTED, "k type %d not supported (F16, BF16, Q8_0)", k->type);
     if (v->type != k->type) return fail(MXFA_ERR_UNSUPPORTED, "k and v types differ (%d, %d)", k->type, v->type);
@@ -187,7 +288,7 @@ int check(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, cons
     const int64_t lim = (int64_t)1 << 30;
     if (q->ne[1] > lim || q->ne[2] > 65535 || q->ne[3] > 65535 || k->ne[1] > lim)
         return fail(MXFA_ERR_UNSUPPORTED, "dimension too large");
-    if (q->nb[0] != 4) return fail(MXFA_ERR_UNSUPPORTED, "q rows must be contiguous");
+    if (q->nb[0] != (q16 ? 2u : 4u)) return fail(MXFA_ERR_UNSUPPORTED, "q rows must be contiguous");
     if (k->nb[0] != type_block_bytes(k->type) || v->nb[0] != type_block_bytes(v->type))
         return fail(MXFA_ERR_UNSUPPORTED, "k/v rows must be contiguous");
     if (!q->data || !k->data || !v->data) return fail(MXFA_ERR_INVALID, "NULL data pointer");
@@ -265,6 +366,7 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     a.mask = mask ? (const char *)mask->data : nullptr;
     a.dst = dst ? (float *)dst->data : nullptr;
     a.q_nb1 = (int64_t)q->nb[1]; a.q_nb2 = (int64_t)q->nb[2]; a.q_nb3 = (int64_t)q->nb[3];
+    a.q16 = q->type != MXFA_TYPE_F32;
     a.k_nb1 = (int64_t)k->nb[1]; a.k_nb2 = (int64_t)k->nb[2]; a.k_nb3 = (int64_t)k->nb[3];
     a.v_nb1 = (int64_t)v->nb[1]; a.v_nb2 = (int64_t)v->nb[2]; a.v_nb3 = (int64_t)v->nb[3];
     if (mask) {
@@ -597,6 +699,21 @@ int mxfa_flash_attn_ext_masked(const mxfa_tensor *q, const mxfa_tensor *k, const
     rc = check_spec(mask, q);
     if (rc != MXFA_OK) return rc;
     return run(q, k, v, nullptr, params, dst, hip_stream, mask);
+}
+
+int mxfa_qk_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *q_norm,
+                      const mxfa_tensor *k_norm, const mxfa_tensor *positions, const mxfa_norm_rope_params *params,
+                      mxfa_tensor *q_out, mxfa_tensor *k_out, mxfa_tensor *v_out, const mxfa_tensor *rows,
+                      void *hip_stream) {
+    NormRopeArgs a;
+    int ot = 0;
+    const int rc = check_norm_rope(q, k, v, q_norm, k_norm, positions, params, q_out, k_out, v_out, rows, &a, &ot);
+    if (rc != MXFA_OK) return rc;
+    hipStream_t stream = (hipStream_t)hip_stream;
+    const hipError_t e =
+        timed_launch("qk_norm_rope", stream, [&] { return launch_qk_norm_rope(a, ot, stream); });
+    if (e != hipSuccess) return fail(MXFA_ERR_HIP, "qk_norm_rope launch: %s", hipGetErrorString(e));
+    return MXFA_OK;
 }
 
 int mxfa_set_rows_supports(const mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_tensor *rows) {

@@ -70,6 +70,7 @@ struct FaArgs {
     int32_t n_qt, n_kt;                   // tiles along Sq and Skv
     int32_t n_kt_pad;                     // class row stride (n_kt rounded up to 4)
     // structured mask (sm_flags == 0: none; then `mask` may hold a dense one)
+    int32_t q16;                          // Q stored in K's 16-bit type (no conversion on load)
     int32_t sm_flags, sm_window, sm_pos0, sm_nlen;
     int32_t sm_len[kSmMaxLen];
 };

@@ -50,6 +50,27 @@ struct SetRowsArgs {
 // n_rows * cpr < 2^31.
 hipError_t launch_set_rows(const SetRowsArgs &a, int dtype, hipStream_t stream);
 
+// Pre-attention fusion (QK-RMSNorm, NEOX RoPE, 16-bit cast, KV-cache
+// write); see qk_norm_rope.hip.  Q/K/V rows are F32 [128, H, S, B] with
+// strides {head, token, batch}; Q goes to [128, Nh, S, B] contiguous, K/V to
+// row rows[s, b % r_ne1] (or s) of their [128, kv_rows, Nkv, B] views.
+struct NormRopeArgs {
+    const char *q, *k, *v;
+    int64_t q_nb[3], k_nb[3], v_nb[3];
+    const float *q_w, *k_w;
+    const int32_t *pos;
+    int32_t pos_per_batch;
+    float eps, theta_scale;
+    int32_t clamp_v;
+    char *q_out, *k_out, *v_out;
+    int64_t kv_nb1, kv_nb2, kv_nb3, kv_rows;
+    const char *rows;
+    int64_t r_nb0, r_nb1;
+    int32_t r_ne1, rows_i64;
+    int32_t Nh, Nkv, S, B;
+};
+hipError_t launch_qk_norm_rope(const NormRopeArgs &a, int out_type, hipStream_t stream);
+
 // Per-kernel timing: when enabled, timed_launch() brackets `launch` with
 // two events on `stream` and files them under `family`.
 bool timing_enabled();

@@ -1,0 +1,152 @@
+// qk_norm_rope.hip -- the work between the QKV projections and attention,
+// fused into one pass: QK-RMSNorm, NEOX RoPE, the 16-bit cast of Q, K and V,
+// and the KV-cache write.
+//
+// The reference runs it as separate ggml ops per layer (src/qwen3-lm.h:418-454;
+// src/dit-graph.h:177-225):
+//   q = rope_neox(rms_norm(q, eps) * q_norm, pos);  k likewise with k_norm
+//   k, v = cont(permute(...)); v = clamp(v, +-65504) (optional, :438-441)
+//   set_rows(cache_k, k, kv_rows); set_rows(cache_v, v, kv_rows)
+// after which attention reads Q in F32 and converts it to K's type.  Here
+// every row of 128 values is read once in F32 and written once in 16 bits:
+// Q into [D, Nh, S, B] (attention takes its permuted view, as the reference
+// does), K and V straight into their cache rows.
+//
+// Arithmetic as ggml's CPU ops do it:
+//   rms_norm: sum of x*x (float products) accumulated in double, mean =
+//     sum / 128, scale = 1 / sqrtf(mean + eps), y = x * scale, then * w;
+//   rope (NEOX, n_dims = 128, freq_scale 1, no YaRN): the angle of pair i
+//     (dims i, i + 64) is theta_i = p * theta_scale^i formed by repeated
+//     float multiplication from theta_0 = p, theta_scale = powf(base, -2/128)
+//     (host); y_i = x_i cos - x_{i+64} sin, y_{i+64} = x_i sin + x_{i+64} cos;
+//   16-bit cast: round to nearest even.
+
+#include "mxfa_common.h"
+#include "mxfa_internal.h"
+
+namespace mxfa {
+
+template <int OT>
+__device__ __forceinline__ uint16_t to16(float x) {
+    return Mfma16<OT>::from_f32(x);
+}
+
+// Rows of one token: [0, Nh) Q heads, [Nh, Nh + Nkv) K heads, then V heads.
+constexpr int kGroups = 3;   // 16-row groups a workgroup loads before it computes (48-row tokens: one pass)
+
+// One workgroup per token (s, b), 4 waves.  A row belongs to 16 lanes: lane
+// j of the 16 holds dims 4j..4j+3 and 64+4j..64+4j+3 (the pairs it rotates,
+// two 16-byte loads), so a wave covers 4 rows per step and the row's sum of
+// squares takes 4 cross-lane steps.  Row h = 16 g + 4 wave + lane / 16 for
+// group g.  The angles of the lane's 4 pairs depend on the token's position
+// only: their chain of multiplications and sin/cos are formed once per
+// token while the row loads are in flight.
+template <int OT>
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(const NormRopeArgs a) {
+    // (no contraction into fma: each product and sum rounds as written)
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 15, sub = lane >> 4;
+    const int s = (int)(blockIdx.x % (unsigned)a.S), b = (int)(blockIdx.x / (unsigned)a.S);
+    const int H = a.Nh + 2 * a.Nkv;
+
+    // K/V destination row of this token (uniform); out of range: skipped
+    int64_t r = s;
+    if (a.rows) {
+        const char *ip = a.rows + (int64_t)s * a.r_nb0 + (int64_t)(b % a.r_ne1) * a.r_nb1;
+        r = a.rows_i64 ? *(const int64_t *)ip : (int64_t)*(const int32_t *)ip;
+    }
+    const bool kv_ok = r >= 0 && r < a.kv_rows;
+    const int pos = a.pos[s + (int64_t)(a.pos_per_batch ? b : 0) * a.S];
+
+    for (int g0 = 0; g0 < H; g0 += 16 * kGroups) {
+        f32x4 lo[kGroups], hi[kGroups];
+        int kind[kGroups], hh[kGroups];
+#pragma unroll
+        for (int g = 0; g < kGroups; g++) {
+            const int h = g0 + 16 * g + 4 * wave + sub;
+            lo[g] = hi[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+            kind[g] = h < a.Nh ? 0 : (h < a.Nh + a.Nkv ? 1 : (h < H ? 2 : 3));
+            hh[g] = kind[g] == 0 ? h : (kind[g] == 1 ? h - a.Nh : h - a.Nh - a.Nkv);
+            if (kind[g] < 3) {
+                const char *src = kind[g] == 0 ? a.q : (kind[g] == 1 ? a.k : a.v);
+                const int64_t *nb = kind[g] == 0 ? a.q_nb : (kind[g] == 1 ? a.k_nb : a.v_nb);
+                const float *x = (const float *)(src + (int64_t)hh[g] * nb[0] + (int64_t)s * nb[1] +
+                                                 (int64_t)b * nb[2]);
+                lo[g] = *(const f32x4 *)(x + 4 * j);
+                hi[g] = *(const f32x4 *)(x + 64 + 4 * j);
+            }
+        }
+        const f32x4 qw0 = *(const f32x4 *)(a.q_w + 4 * j), qw1 = *(const f32x4 *)(a.q_w + 64 + 4 * j);
+        const f32x4 kw0 = *(const f32x4 *)(a.k_w + 4 * j), kw1 = *(const f32x4 *)(a.k_w + 64 + 4 * j);
+        // angles of pairs 4j..4j+3: `pair` float multiplications from theta_0 = pos
+        float th[4] = {0.f, 0.f, 0.f, 0.f}, t = (float)pos;
+#pragma unroll
+        for (int i = 0; i < 64; i++) {
+            th[i & 3] = (i >> 2) == j ? t : th[i & 3];
+            t *= a.theta_scale;
+        }
+        float sn[4], cs[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) sincosf(th[e], &sn[e], &cs[e]);
+#pragma unroll
+        for (int g = 0; g < kGroups; g++) {
+            if (g0 + 16 * g >= H) break;   // wave-uniform
+            float y0[4], y1[4];
+            // rms_norm: the row's sum of squares (float products) in double
+            double ss = 0.0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                y0[e] = lo[g][e];
+                y1[e] = hi[g][e];
+                ss += (double)(y0[e] * y0[e]);
+                ss += (double)(y1[e] * y1[e]);
+            }
+#pragma unroll
+            for (int off = 8; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+            const int kd = kind[g];
+            if (kd < 2) {
+                const float mean = (float)(ss / 128.0);
+                const float scale = 1.0f / sqrtf(mean + a.eps);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float w0 = kd == 0 ? qw0[e] : kw0[e], w1 = kd == 0 ? qw1[e] : kw1[e];
+                    const float u0 = (y0[e] * scale) * w0, u1 = (y1[e] * scale) * w1;
+                    y0[e] = u0 * cs[e] - u1 * sn[e];
+                    y1[e] = u0 * sn[e] + u1 * cs[e];
+                }
+            } else if (a.clamp_v) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    y0[e] = fminf(fmaxf(y0[e], -65504.0f), 65504.0f);
+                    y1[e] = fminf(fmaxf(y1[e], -65504.0f), 65504.0f);
+                }
+            }
+            u32x2 w0, w1;
+            w0[0] = (uint32_t)to16<OT>(y0[0]) | ((uint32_t)to16<OT>(y0[1]) << 16);
+            w0[1] = (uint32_t)to16<OT>(y0[2]) | ((uint32_t)to16<OT>(y0[3]) << 16);
+            w1[0] = (uint32_t)to16<OT>(y1[0]) | ((uint32_t)to16<OT>(y1[1]) << 16);
+            w1[1] = (uint32_t)to16<OT>(y1[2]) | ((uint32_t)to16<OT>(y1[3]) << 16);
+            char *row = nullptr;
+            if (kd == 0) row = a.q_out + (((int64_t)b * a.S + s) * a.Nh + hh[g]) * 256;
+            else if (kd < 3 && kv_ok)
+                row = (kd == 1 ? a.k_out : a.v_out) + r * a.kv_nb1 + (int64_t)hh[g] * a.kv_nb2 + (int64_t)b * a.kv_nb3;
+            if (row) {
+                *(u32x2 *)(row + 8 * j) = w0;
+                *(u32x2 *)(row + 128 + 8 * j) = w1;
+            }
+        }
+    }
+}
+
+hipError_t launch_qk_norm_rope(const NormRopeArgs &a, int out_type, hipStream_t stream) {
+    const int64_t tokens = (int64_t)a.S * a.B;
+    if (tokens <= 0) return hipSuccess;
+    const dim3 grid((unsigned)tokens);
+    if (out_type == T_F16) hipLaunchKernelGGL(qk_norm_rope_kernel<T_F16>, grid, dim3(256), 0, stream, a);
+    else if (out_type == T_BF16) hipLaunchKernelGGL(qk_norm_rope_kernel<T_BF16>, grid, dim3(256), 0, stream, a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace mxfa

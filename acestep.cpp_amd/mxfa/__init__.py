@@ -41,6 +41,7 @@ EXPORTED_SYMBOLS = (
     "mxfa_supports_masked",
     "mxfa_flash_attn_ext_masked",
     "mxfa_reserve",
+    "mxfa_qk_norm_rope",
     "mxfa_set_rows_supports",
     "mxfa_set_rows",
     "mxfa_release",
@@ -69,6 +70,10 @@ class MxfaParams(ctypes.Structure):
         ("logit_softcap", ctypes.c_float),
         ("prec", ctypes.c_int32),
     ]
+
+
+class MxfaNormRopeParams(ctypes.Structure):
+    _fields_ = [("eps", ctypes.c_float), ("freq_base", ctypes.c_float), ("clamp_v", ctypes.c_int32)]
 
 
 MASK_CAUSAL, MASK_WINDOW, MASK_LENGTHS = 1, 2, 4
@@ -117,6 +122,9 @@ def _load():
     L.mxfa_supports.restype = ctypes.c_int
     L.mxfa_flash_attn_ext.argtypes = [P, P, P, P, ctypes.POINTER(MxfaParams), P, ctypes.c_void_p]
     L.mxfa_flash_attn_ext.restype = ctypes.c_int
+    L.mxfa_qk_norm_rope.argtypes = [P, P, P, P, P, P, ctypes.POINTER(MxfaNormRopeParams), P, P, P, P,
+                                    ctypes.c_void_p]
+    L.mxfa_qk_norm_rope.restype = ctypes.c_int
     L.mxfa_reserve.argtypes = [P, P, P, P, ctypes.POINTER(MxfaParams), ctypes.c_void_p]
     L.mxfa_reserve.restype = ctypes.c_int
     L.mxfa_set_rows_supports.argtypes = [P, P, P]
@@ -225,6 +233,27 @@ def flash_attn_ext(q, k, v, mask, scale, max_bias=0.0, logit_softcap=0.0, prec=P
     if rc != OK:
         raise MxfaError(rc, last_error())
     return dst
+
+
+def qk_norm_rope(q, k, v, q_norm, k_norm, positions, eps, freq_base, q_out, k_out, v_out, rows=None,
+                 clamp_v=False, stream: Optional[int] = None) -> None:
+    """The pre-attention work of a layer in one kernel (mxfa_qk_norm_rope):
+    QK-RMSNorm, NEOX RoPE, 16-bit cast of Q/K/V, K/V written into their
+    cache rows.  All arguments are DeviceViews (rows may be None)."""
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    ds = [t.desc() for t in (q, k, v, q_norm, k_norm, positions, q_out, k_out, v_out)]
+    dr = rows.desc() if rows is not None else None
+    p = MxfaNormRopeParams()
+    p.eps, p.freq_base, p.clamp_v = float(eps), float(freq_base), int(bool(clamp_v))
+    refs = [ctypes.byref(d) for d in ds]
+    rc = lib.mxfa_qk_norm_rope(refs[0], refs[1], refs[2], refs[3], refs[4], refs[5], ctypes.byref(p), refs[6],
+                               refs[7], refs[8], ctypes.byref(dr) if dr is not None else None,
+                               ctypes.c_void_p(int(stream)))
+    if rc != OK:
+        raise MxfaError(rc, last_error())
 
 
 def reserve(q, k, v, mask, scale, max_bias=0.0, logit_softcap=0.0, prec=PREC_F32, stream=None) -> None:

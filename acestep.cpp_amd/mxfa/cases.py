@@ -303,6 +303,28 @@ def c5(**kw) -> FaCase:
 BUILDERS = {"c1": c1, "c2": c2, "c3": c3, "c4s": c4_self, "c4x": c4_cross, "c5": c5}
 
 
+def with_q16(case: FaCase) -> FaCase:
+    """A copy of `case` whose Q is stored in K's 16-bit type (F16 / BF16),
+    rounded to nearest even, same element layout: what the fused
+    pre-attention step hands attention (mxfa_qk_norm_rope)."""
+    assert case.k.type in (TYPE_F16, TYPE_BF16) and case.q.type == TYPE_F32 and case.q.offset % 4 == 0
+    bits = _kv16(np.ascontiguousarray(case.q.buf).view(np.float32), case.k.type)
+    q = HostView(case.k.type, tuple(case.q.ne), tuple(int(x) // 2 for x in case.q.nb), bits, case.q.offset // 2)
+    return FaCase(case.name, q, case.k, case.v, case.mask, case.scale, case.max_bias, case.softcap, dict(case.meta))
+
+
+def norm_rope_work(B: int, S: int, Nh: int, Nkv: int, rows_i64: bool = True) -> dict:
+    """Algorithmic bytes of one fused pre-attention call (mxfa_qk_norm_rope):
+    every F32 row of Q, K and V read once, its 16-bit row written once, the
+    positions and row ids read once (the two 512 B weights are noise).  The
+    reference's op chain (rms_norm, mul, rope, cont, clamp, set_rows, and
+    attention's F32 Q read) moves several times that."""
+    n = (Nh + 2 * Nkv) * S * B
+    rd, wr = n * 4 * D, n * 2 * D
+    ids = S * B * 4 + S * B * (8 if rows_i64 else 4)
+    return dict(rows=n, read_bytes=rd, write_bytes=wr, id_bytes=ids, bytes=rd + wr + ids)
+
+
 # -- structured masks ------------------------------------------------------------
 
 def structured_spec(case: FaCase) -> dict:
@@ -497,7 +519,7 @@ def work(case: FaCase) -> dict:
             kv_rows += int(any_key.sum())
     row_kv = _type_row_bytes(case.k.type, D) + _type_row_bytes(case.v.type, D)
     kv_bytes = kv_rows * row_kv
-    q_bytes = D * Sq * Nh * B * 4
+    q_bytes = _type_row_bytes(case.q.type, D) * Sq * Nh * B
     o_bytes = D * Sq * Nh * B * 4
     m_bytes = 0 if case.mask is None else int(case.mask.ne[2] * case.mask.ne[3]) * Sq * Skv * 2
     return dict(flops=4 * D * pairs, pairs=pairs, kv_bytes=kv_bytes,

@@ -22,7 +22,9 @@ HBM peak), and so are the structured-mask variants c2m / c3m / c4xm (the
 same work with the mask given as metadata: mxfa_flash_attn_ext_masked) and
 the KV-cache writes that precede C2 / C3 (GGML_OP_SET_ROWS:
 kw2, kw3, and kw5 into a Q8_0 cache; GB/s of F32 read + converted row
-written + row ids, vs the HBM peak).  Inputs of bandwidth-bound configs are rotated over enough device
+written + row ids, vs the HBM peak), the fused pre-attention step of C2
+(nr2: QK-RMSNorm + RoPE + F16 cast + cache write, GB/s vs the HBM peak) and
+C2's attention on the F16 Q that step writes (c2q).  Inputs of bandwidth-bound configs are rotated over enough device
 copies that consecutive steps do not hit in the 256 MB Infinity Cache.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2,c3] [--no-cpu]
@@ -65,11 +67,14 @@ DESCR.update({
     "kw2": "KV-cache write (GGML_OP_SET_ROWS) of C2: 2048 tokens x 8 KV heads, F32 -> F16 cache [128, 2048, 8]",
     "kw3": "KV-cache write of C3: 1 token x 8 KV heads for each of 8 sets, F32 -> F16 4D cache view",
     "kw5": "KV-cache write of C2 into a Q8_0 cache: 2048 tokens x 8 KV heads, F32 -> Q8_0",
+    "nr2": "pre-attention step of C2 (mxfa_qk_norm_rope): QK-RMSNorm + NEOX RoPE + F16 cast of 2048 tokens x "
+           "(32 Q + 8 K + 8 V heads), Q out [128, 32, 2048], K/V into their cache rows",
+    "c2q": "C2 with Q in F16 as the pre-attention step writes it (no F32 Q read, no conversion)",
 })
 BOUND = {"c1": "hbm", "c2": "mfma", "c3": "hbm", "c4s": "mfma", "c4x": "hbm", "c5": "hbm",
-         "c2m": "mfma", "c3m": "hbm", "c4xm": "hbm"}
+         "c2m": "mfma", "c3m": "hbm", "c4xm": "hbm", "c2q": "mfma"}
 KERNEL = {"c1": "fa_decode", "c2": "fa_prefill", "c3": "fa_decode", "c4s": "fa_prefill", "c4x": "fa_prefill",
-          "c5": "fa_decode", "c2m": "fa_prefill", "c3m": "fa_decode", "c4xm": "fa_prefill"}
+          "c5": "fa_decode", "c2m": "fa_prefill", "c3m": "fa_decode", "c4xm": "fa_prefill", "c2q": "fa_prefill"}
 STRUCTURED = {"c2m": "c2", "c3m": "c3", "c4xm": "c4x"}   # structured-mask variant -> dense config
 
 
@@ -177,6 +182,68 @@ def time_set_rows(mx, torch, case, steps, warmup, rotate_bytes=ROTATE_BYTES):
     torch.cuda.synchronize()
     mx.timing_enable(False)
     tot, n = mx.timing_read("set_rows")
+    mx.timing_reset()
+    del copies
+    torch.cuda.empty_cache()
+    return ms, (tot / n if n else None), w, n_copies
+
+
+def time_norm_rope(mx, torch, steps, warmup, B=1, S=2048, Nh=32, Nkv=8, max_seq=2048,
+                   rotate_bytes=ROTATE_BYTES):
+    """Fused pre-attention step timing on synthetic device data: (ms per call,
+    kernel avg ms, work, copies).  Copies rotate past the Infinity Cache."""
+    from mxfa import cases as C
+
+    D = 128
+    H = Nh + 2 * Nkv
+    w = C.norm_rope_work(B, S, Nh, Nkv)
+    n_copies = int(min(32, max(1, math.ceil(rotate_bytes / w["bytes"]))))
+    g = torch.Generator(device="cuda").manual_seed(1201)
+    qw = torch.ones(D, device="cuda") + 0.1 * torch.randn(D, device="cuda", generator=g)
+    kw = torch.ones(D, device="cuda") + 0.1 * torch.randn(D, device="cuda", generator=g)
+    pos = torch.arange(S, dtype=torch.int32, device="cuda")
+    rows = torch.arange(S, dtype=torch.int64, device="cuda")
+    wnb = (4, 4 * D, 4 * D, 4 * D)
+    dqw, dkw = mx.DeviceView(0, (D, 1, 1, 1), wnb, qw.data_ptr(), qw), mx.DeviceView(0, (D, 1, 1, 1), wnb, kw.data_ptr(), kw)
+    dpos = mx.DeviceView(26, (S, 1, 1, 1), (4, 4 * S, 4 * S, 4 * S), pos.data_ptr(), pos)
+    drows = mx.DeviceView(27, (S, 1, 1, 1), (8, 8 * S, 8 * S, 8 * S), rows.data_ptr(), rows)
+    copies = []
+    for _ in range(n_copies):
+        x = torch.randn(B, S, H, D, device="cuda", generator=g)
+        qo = torch.empty(B, S, Nh, D, dtype=torch.float16, device="cuda")
+        kc = torch.empty(B, Nkv, max_seq, D, dtype=torch.float16, device="cuda")
+        vc = torch.empty_like(kc)
+        xnb = (4, 4 * D, 4 * D * H, 4 * D * H * S)
+        cnb = (2, 2 * D, 2 * D * max_seq, 2 * D * max_seq * Nkv)
+        copies.append((mx.DeviceView(0, (D, Nh, S, B), xnb, x.data_ptr(), x),
+                       mx.DeviceView(0, (D, Nkv, S, B), xnb, x.data_ptr() + 4 * D * Nh, x),
+                       mx.DeviceView(0, (D, Nkv, S, B), xnb, x.data_ptr() + 4 * D * (Nh + Nkv), x),
+                       mx.DeviceView(1, (D, Nh, S, B), (2, 2 * D, 2 * D * Nh, 2 * D * Nh * S), qo.data_ptr(), qo),
+                       mx.DeviceView(1, (D, max_seq, Nkv, B), cnb, kc.data_ptr(), kc),
+                       mx.DeviceView(1, (D, max_seq, Nkv, B), cnb, vc.data_ptr(), vc)))
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step(i):
+        q, k, v, qo, ko, vo = copies[i % n_copies]
+        mx.qk_norm_rope(q, k, v, dqw, dkw, dpos, 1e-6, 1e6, qo, ko, vo, drows, stream=stream)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(steps):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    mx.timing_reset()
+    mx.timing_enable(True)
+    for i in range(steps):
+        step(i)
+    torch.cuda.synchronize()
+    mx.timing_enable(False)
+    tot, n = mx.timing_read("qk_norm_rope")
     mx.timing_reset()
     del copies
     torch.cuda.empty_cache()
@@ -358,7 +425,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c2m,c3m,c4xm,kw2,kw3,kw5,dstep")
+    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c2m,c3m,c4xm,c2q,kw2,kw3,kw5,nr2,dstep")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB copy (counter calibration under rocprofv3)")
@@ -390,6 +457,17 @@ def main():
             case = C.SET_ROWS_BUILDERS[name]()
             ms, kms, w, ncp = time_set_rows(mxfa, torch, case, args.steps, args.warmup)
             results[name] = summarize_set_rows(name, ms, kms, w, ncp)
+            log(f"[bench] {name}: {json.dumps(results[name])}")
+            continue
+        if name == "nr2":
+            ms, kms, w, ncp = time_norm_rope(mxfa, torch, args.steps, args.warmup)
+            results[name] = summarize_set_rows(name, ms, kms, w, ncp)
+            log(f"[bench] {name}: {json.dumps(results[name])}")
+            continue
+        if name == "c2q":
+            case = C.with_q16(C.c2())
+            ms, kern, w, ncp = time_case(mxfa, torch, case, args.steps, args.warmup)
+            results[name] = summarize(name, ms, kern, w, ncp)
             log(f"[bench] {name}: {json.dumps(results[name])}")
             continue
         if name == "dstep":

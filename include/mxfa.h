@@ -165,6 +165,43 @@ int mxfa_flash_attn_ext_masked(const mxfa_tensor *q, const mxfa_tensor *k, const
 int mxfa_set_rows_supports(const mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_tensor *rows);
 int mxfa_set_rows(mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_tensor *rows, void *hip_stream);
 
+/* Pre-attention fusion: the work between a layer's QKV projections and its
+ * attention node, in one pass.  The reference runs it as separate ggml ops
+ * (src/qwen3-lm.h:418-454, src/dit-graph.h:177-225):
+ *
+ *   q = rope_neox(rms_norm(q, eps) * q_norm, positions)
+ *   k = rope_neox(rms_norm(k, eps) * k_norm, positions)
+ *   v = clamp(v, -65504, 65504)              (only with clamp_v, :438-441)
+ *   set_rows(cache_k, cont(permute(k)), kv_rows); likewise v
+ *
+ * (rope: n_dims = 128, freq_base, freq_scale 1, no YaRN / ext factor; the
+ * arithmetic of ggml's CPU ops, see qk_norm_rope.hip) and writes Q already
+ * in K's 16-bit type, so that attention (mxfa_flash_attn_ext, Q of K's
+ * type) reads half the bytes and converts nothing:
+ *
+ *   q, k, v   : F32 [128, Nh | Nkv, S, B], nb[0] = 4 (views allowed)
+ *   q_norm, k_norm : F32 [128] contiguous
+ *   positions : I32 [S] (shared by the batches) or [S, B], contiguous
+ *   q_out     : F16 | BF16 [128, Nh, S, B] contiguous (attention takes the
+ *               permuted view [128, S, Nh, B], as the reference does)
+ *   k_out, v_out : the same type, [128, M, Nkv, B] with nb[0] = 2 (a cache
+ *               view); row rows[s, b % R] receives token s of batch b, or
+ *               row s when rows is NULL (then M >= S)
+ *   rows      : I64 | I32 [S, R] with B % R == 0, or NULL
+ *
+ * Row ids outside [0, M) are skipped (ggml asserts).  Launches one kernel
+ * on `hip_stream`, allocates nothing; MXFA_OK or a negative status. */
+typedef struct mxfa_norm_rope_params {
+    float   eps;        /* rms_norm epsilon */
+    float   freq_base;  /* rope theta */
+    int32_t clamp_v;    /* clamp V to +-65504 before the cast */
+} mxfa_norm_rope_params;
+
+int mxfa_qk_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
+                      const mxfa_tensor *q_norm, const mxfa_tensor *k_norm, const mxfa_tensor *positions,
+                      const mxfa_norm_rope_params *params, mxfa_tensor *q_out, mxfa_tensor *k_out,
+                      mxfa_tensor *v_out, const mxfa_tensor *rows, void *hip_stream);
+
 /* HIP graph capture / replay.  The reference replays its static decode
  * graph (src/static-graph.h, src/graph-arena.h, src/qwen3-lm.h:36-58): the
  * node arguments stay at fixed addresses and only their contents change
@@ -199,7 +236,8 @@ int mxfa_version(void);
  * enabled, every kernel the engine launches is bracketed by two HIP events
  * recorded on its launch stream.  mxfa_timing_read() waits for the recorded
  * events, returns the summed duration (ms) and launch count of one kernel
- * family ("fa_prefill", "mask_classify", "fa_decode", "set_rows") since the
+ * family ("fa_prefill", "mask_classify", "fa_decode", "set_rows",
+ * "qk_norm_rope") since the
  * last reset, and mxfa_timing_reset() clears all counters.  Disabled by
  * default; enabling it adds two event records per launch. */
 void mxfa_timing_enable(int on);

@@ -681,3 +681,60 @@ int64_t ora_set_rows(const ora_tensor *dst, const ora_tensor *src, const ora_ten
             }
     return skipped;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Pre-attention work of a layer (reference src/qwen3-lm.h:418-441,           */
+/* src/dit-graph.h:177-225): rms_norm * weight, NEOX rope, V clamp -- the     */
+/* restatement of ggml's published CPU ops (ggml-cpu ops.cpp,                 */
+/* ggml_compute_forward_rms_norm_f32, ggml_compute_forward_rope_f32 with      */
+/* ggml_rope_cache_init / rope_yarn at ext_factor 0, freq_scale 1,            */
+/* attn_factor 1, NEOX pairs (i, i + n_dims/2)); upstream ggml late 2025.    */
+/*   rms_norm: sum (double) of x*x (float), mean = sum/n, scale =             */
+/*     1/sqrtf(mean + eps), y = x*scale, then y*w (ggml_mul);                 */
+/*   rope: theta_scale = powf(base, -2/n_dims); theta_0 = p; theta_{i+1} =    */
+/*     theta_i * theta_scale (float); c = cosf(theta_i), s = sinf(theta_i);  */
+/*     y_i = x_i c - x_{i+n/2} s, y_{i+n/2} = x_i s + x_{i+n/2} c.            */
+/* Inputs: rows of 128 floats; q [B][S][Nh][128] (row (b, s, h) at             */
+/* q + ((b*S + s)*Nh + h)*128), k/v likewise with Nkv; pos [S] or [B][S].     */
+/* Outputs (F32, before the 16-bit cast) in the same layouts.                 */
+/* ------------------------------------------------------------------------ */
+static void norm_rope_row(const float *x, const float *w, int pos, float eps, float theta_scale, float *y) {
+    double sum = 0.0;
+    for (int i = 0; i < 128; i++) sum += (double)(x[i] * x[i]);
+    const float mean = (float)(sum / 128);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    float t[128];
+    for (int i = 0; i < 128; i++) t[i] = x[i] * scale;
+    for (int i = 0; i < 128; i++) t[i] = t[i] * w[i];
+    float theta = (float)pos;
+    for (int i = 0; i < 64; i++) {
+        const float c = cosf(theta), s = sinf(theta);
+        const float x0 = t[i], x1 = t[i + 64];
+        y[i] = x0 * c - x1 * s;
+        y[i + 64] = x0 * s + x1 * c;
+        theta *= theta_scale;
+    }
+}
+
+void ora_qk_norm_rope(const float *q, const float *k, const float *v, const float *qw, const float *kw,
+                      const int32_t *pos, int pos_per_batch, int Nh, int Nkv, int S, int B, float eps,
+                      float freq_base, int clamp_v, float *q_o, float *k_o, float *v_o) {
+    const float theta_scale = powf(freq_base, -2.0f / 128.0f);
+    for (int b = 0; b < B; b++)
+        for (int s = 0; s < S; s++) {
+            const int p = pos[(pos_per_batch ? b * S : 0) + s];
+            for (int h = 0; h < Nh; h++) {
+                const size_t o = (((size_t)b * S + s) * Nh + h) * 128;
+                norm_rope_row(q + o, qw, p, eps, theta_scale, q_o + o);
+            }
+            for (int h = 0; h < Nkv; h++) {
+                const size_t o = (((size_t)b * S + s) * Nkv + h) * 128;
+                norm_rope_row(k + o, kw, p, eps, theta_scale, k_o + o);
+                for (int i = 0; i < 128; i++) {
+                    float x = v[o + i];
+                    if (clamp_v) x = fminf(fmaxf(x, -65504.0f), 65504.0f);
+                    v_o[o + i] = x;
+                }
+            }
+        }
+}

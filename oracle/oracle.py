@@ -11,6 +11,8 @@ fa_ggml(q, k, v, mask, scale, ..., acc_f32=False) -> float32 [B, Sq, Nh, DV]
     acc_f32=True runs the same algorithm with an fp32 V accumulator.
 fa_exact(q, k, v, mask, scale, ...) -> float64 [B, Sq, Nh, DV]
     fp64 two-pass softmax reference of the same op.
+qk_norm_rope(q, k, v, q_w, k_w, pos, eps, base, clamp_v) -> (q, k, v) F32
+    restatement of ggml's CPU rms_norm * weight + NEOX rope (+ V clamp).
 set_rows(dst, src, rows) -> skipped rows
     restatement of ggml's CPU set_rows (the KV-cache write), in place on dst.
 
@@ -90,6 +92,8 @@ def lib():
             getattr(L, name).argtypes = [ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
             getattr(L, name).restype = ctypes.c_float
         L.ora_mad_f16.argtypes = [ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float]
+        L.ora_qk_norm_rope.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_int] * 5 + [ctypes.c_float] * 2 + \
+            [ctypes.c_int] + [ctypes.c_void_p] * 3
         L.ora_set_rows.argtypes = [P, P, P]
         L.ora_set_rows.restype = ctypes.c_int64
         L.ora_set_force_scalar.argtypes = [ctypes.c_int]
@@ -205,3 +209,25 @@ def set_rows(dst: HostTensor, src: HostTensor, rows: HostTensor) -> int:
     if n < 0:
         raise ValueError("ora_set_rows rejected the shapes")
     return int(n)
+
+
+# -- pre-attention work (rms_norm, NEOX rope) ----------------------------------
+
+def qk_norm_rope(q, k, v, q_w, k_w, pos, eps, freq_base, clamp_v=False):
+    """q [B, S, Nh, 128], k/v [B, S, Nkv, 128] float32, pos [S] or [B, S]
+    int32: returns the F32 rows ggml's ops produce before the 16-bit cast."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    q_w = np.ascontiguousarray(q_w, dtype=np.float32)
+    k_w = np.ascontiguousarray(k_w, dtype=np.float32)
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    B, S, Nh, D = q.shape
+    Nkv = k.shape[2]
+    assert D == 128 and k.shape == (B, S, Nkv, 128) and v.shape == k.shape
+    per_batch = int(pos.ndim == 2)
+    qo, ko, vo = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+    lib().ora_qk_norm_rope(q.ctypes.data, k.ctypes.data, v.ctypes.data, q_w.ctypes.data, k_w.ctypes.data,
+                           pos.ctypes.data, per_batch, Nh, Nkv, S, B, eps, freq_base, int(bool(clamp_v)),
+                           qo.ctypes.data, ko.ctypes.data, vo.ctypes.data)
+    return qo, ko, vo
