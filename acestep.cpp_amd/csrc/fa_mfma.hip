@@ -55,6 +55,7 @@ constexpr int kTileBytes = 16384;            // K or V rows of one 64-key tile
 constexpr int kStageBytes = 2 * kTileBytes;  // K + V
 constexpr int kPfLds = 2 * kStageBytes;      // double buffered: 64 KB
 constexpr uint32_t kXcds = 8;                // MI355X: workgroups go round-robin to 8 XCDs
+constexpr uint32_t kCusPerXcd = 32;          // 256 CUs
 
 __global__ void __launch_bounds__(256) mask_classify_kernel(const FaArgs a, uint8_t *cls) {
     // One workgroup per (key tile, query tile, mask plane).  Each row of the
@@ -230,7 +231,14 @@ fa_prefill_kernel(const FaArgs a) {
     {
         const uint32_t L = __builtin_amdgcn_workgroup_id_x();
         const uint32_t N = (uint32_t)(a.n_qt * a.Nh * a.B);
-        const uint32_t nq = N / kXcds, nr = N % kXcds, x = L % kXcds, s = L / kXcds;
+        const uint32_t nq = N / kXcds, nr = N % kXcds, x = L % kXcds, s0 = L / kXcds;
+        // Snake order over rounds of kCusPerXcd: the XCD's dispatcher gives
+        // each CU one workgroup per round, so odd rounds run reversed and a
+        // CU pairs a long causal tile with a short one.
+        const uint32_t n_x = x < nr ? nq + 1 : nq;
+        const uint32_t rnd = s0 / kCusPerXcd, w = s0 % kCusPerXcd;
+        const uint32_t cnt = min(kCusPerXcd, n_x - rnd * kCusPerXcd);
+        const uint32_t s = (rnd & 1) ? rnd * kCusPerXcd + (cnt - 1 - w) : s0;
         const uint32_t J = x < nr ? x * (nq + 1) + s : nr * (nq + 1) + (x - nr) * nq + s;
         const uint32_t per_u = (uint32_t)(a.G * a.n_qt);
         const uint32_t u = J / per_u, r = J % per_u;
