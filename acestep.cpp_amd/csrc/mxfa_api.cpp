@@ -716,6 +716,16 @@ int mxfa_qk_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_ten
     return MXFA_OK;
 }
 
+int mxfa_qk_norm_rope_supports(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
+                               const mxfa_tensor *q_norm, const mxfa_tensor *k_norm, const mxfa_tensor *positions,
+                               const mxfa_norm_rope_params *params, const mxfa_tensor *q_out,
+                               const mxfa_tensor *k_out, const mxfa_tensor *v_out, const mxfa_tensor *rows) {
+    return check_norm_rope(q, k, v, q_norm, k_norm, positions, params, q_out, k_out, v_out, rows, nullptr,
+                           nullptr) == MXFA_OK
+               ? 1
+               : 0;
+}
+
 int mxfa_set_rows_supports(const mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_tensor *rows) {
     return check_set_rows(dst, src, rows, nullptr) == MXFA_OK ? 1 : 0;
 }

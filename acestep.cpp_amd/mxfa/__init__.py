@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "mxfa_flash_attn_ext_masked",
     "mxfa_reserve",
     "mxfa_qk_norm_rope",
+    "mxfa_qk_norm_rope_supports",
     "mxfa_set_rows_supports",
     "mxfa_set_rows",
     "mxfa_release",
@@ -125,6 +126,8 @@ def _load():
     L.mxfa_qk_norm_rope.argtypes = [P, P, P, P, P, P, ctypes.POINTER(MxfaNormRopeParams), P, P, P, P,
                                     ctypes.c_void_p]
     L.mxfa_qk_norm_rope.restype = ctypes.c_int
+    L.mxfa_qk_norm_rope_supports.argtypes = [P, P, P, P, P, P, ctypes.POINTER(MxfaNormRopeParams), P, P, P, P]
+    L.mxfa_qk_norm_rope_supports.restype = ctypes.c_int
     L.mxfa_reserve.argtypes = [P, P, P, P, ctypes.POINTER(MxfaParams), ctypes.c_void_p]
     L.mxfa_reserve.restype = ctypes.c_int
     L.mxfa_set_rows_supports.argtypes = [P, P, P]

@@ -197,6 +197,15 @@ typedef struct mxfa_norm_rope_params {
     int32_t clamp_v;    /* clamp V to +-65504 before the cast */
 } mxfa_norm_rope_params;
 
+/* 1 when mxfa_qk_norm_rope would accept these descriptors (checks only,
+ * nothing is dereferenced or launched), else 0 with the reason in
+ * mxfa_last_error(): the supports_op of the fused step, so that a caller
+ * keeps the reference's op chain for what it does not take. */
+int mxfa_qk_norm_rope_supports(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
+                               const mxfa_tensor *q_norm, const mxfa_tensor *k_norm, const mxfa_tensor *positions,
+                               const mxfa_norm_rope_params *params, const mxfa_tensor *q_out,
+                               const mxfa_tensor *k_out, const mxfa_tensor *v_out, const mxfa_tensor *rows);
+
 int mxfa_qk_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
                       const mxfa_tensor *q_norm, const mxfa_tensor *k_norm, const mxfa_tensor *positions,
                       const mxfa_norm_rope_params *params, mxfa_tensor *q_out, mxfa_tensor *k_out,

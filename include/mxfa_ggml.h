@@ -15,6 +15,9 @@
  *     mxfa_ggml_set_rows_supports(node)        -> 1 / 0
  *     mxfa_ggml_set_rows(node, stream)         -> MXFA_OK / negative status
  *
+ * and, where a model hands its pre-attention chain over as one custom node
+ * (layout below), mxfa_ggml_qk_norm_rope_supports / mxfa_ggml_qk_norm_rope.
+ *
  * The node layout is the one ggml_flash_attn_ext builds (upstream ggml; the
  * reference's call sites are src/qwen3-lm.h:465-469, :789-794,
  * src/dit-graph.h:227-231, :348-352, src/qwen3-enc.h:195-199):
@@ -118,6 +121,46 @@ static inline int mxfa_ggml_flash_attn_ext(const struct ggml_tensor *node, void 
     rc = mxfa_ggml_unpack(node, &q, &k, &v, &m, &mp, &d, &p);
     if (rc != 0) return rc;
     return mxfa_flash_attn_ext(&q, &k, &v, mp, &p, &d, hip_stream);
+}
+
+/* The pre-attention step (src/qwen3-lm.h:418-454: rms_norm, mul, rope_ext,
+ * permute, cont, clamp, and the two set_rows) as one custom node, e.g.
+ * ggml_custom_4d with these sources, in this order:
+ *   node    = Q out [128, Nh, S, B], F16 or BF16 (attention takes its
+ *             permuted view, as it took the rope output's);
+ *   src[0..2] = q, k, v: the F32 projections [128, Nh|Nkv, S, B];
+ *   src[3], src[4] = q_norm, k_norm: F32 [128];
+ *   src[5] = positions: I32 [S] or [S, B];
+ *   src[6], src[7] = the K and V cache views written, [128, M, Nkv, B];
+ *   src[8] = row ids I64/I32 [S, R], or NULL (row s).
+ * eps, rope base and the V clamp are not op_params of a custom node; the
+ * caller passes them (from its user data). */
+static inline int mxfa_ggml_unpack_norm_rope(const struct ggml_tensor *node, mxfa_tensor *t /* [10] */,
+                                             const mxfa_tensor **rows) {
+    int i;
+    if (!node) return MXFA_ERR_INVALID;
+    for (i = 0; i < 8; i++)
+        if (!node->src[i]) return MXFA_ERR_INVALID;
+    for (i = 0; i < 8; i++) mxfa_ggml_desc(node->src[i], &t[i]);
+    mxfa_ggml_desc(node, &t[8]);
+    *rows = mxfa_ggml_desc(node->src[8], &t[9]);
+    return 0;
+}
+
+static inline int mxfa_ggml_qk_norm_rope_supports(const struct ggml_tensor *node, const mxfa_norm_rope_params *p) {
+    mxfa_tensor t[10];
+    const mxfa_tensor *rows;
+    if (mxfa_ggml_unpack_norm_rope(node, t, &rows) != 0) return 0;
+    return mxfa_qk_norm_rope_supports(&t[0], &t[1], &t[2], &t[3], &t[4], &t[5], p, &t[8], &t[6], &t[7], rows);
+}
+
+static inline int mxfa_ggml_qk_norm_rope(const struct ggml_tensor *node, const mxfa_norm_rope_params *p,
+                                         void *hip_stream) {
+    mxfa_tensor t[10];
+    const mxfa_tensor *rows;
+    const int rc = mxfa_ggml_unpack_norm_rope(node, t, &rows);
+    if (rc != 0) return rc;
+    return mxfa_qk_norm_rope(&t[0], &t[1], &t[2], &t[3], &t[4], &t[5], p, &t[8], &t[6], &t[7], rows, hip_stream);
 }
 
 #ifdef __cplusplus

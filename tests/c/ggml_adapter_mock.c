@@ -87,5 +87,36 @@ int main(int argc, char **argv) {
     printf("set_rows_bad_ids %d\n", mxfa_ggml_set_rows_supports(&sr));
     sr.src[1] = NULL;
     printf("set_rows_no_ids %d %d\n", mxfa_ggml_set_rows_supports(&sr), mxfa_ggml_set_rows(&sr, NULL));
+
+    /* the pre-attention step of a 4B-LM layer as one custom node
+     * (src/qwen3-lm.h:418-454): 7 tokens, 32 / 8 heads, 2048-slot caches */
+    struct ggml_tensor nq, nk, nv, qw, kw, pos, ck, cv, rid, qo;
+    struct ggml_tensor *all[] = {&nq, &nk, &nv, &qw, &kw, &pos, &ck, &cv, &rid, &qo};
+    for (int i = 0; i < 10; i++) memset(all[i], 0, sizeof *all[i]);
+    nq.type = 0; set4(nq.ne, 128, 32, 7, 1); contig(&nq, 4); nq.data = (void *)(uintptr_t)0x800000;
+    nk.type = 0; set4(nk.ne, 128, 8, 7, 1); contig(&nk, 4); nk.data = (void *)(uintptr_t)0x900000;
+    nv = nk; nv.data = (void *)(uintptr_t)0xA00000;
+    qw.type = 0; set4(qw.ne, 128, 1, 1, 1); contig(&qw, 4); qw.data = (void *)(uintptr_t)0xB00000;
+    kw = qw; kw.data = (void *)(uintptr_t)0xB10000;
+    pos.type = 26; set4(pos.ne, 7, 1, 1, 1); contig(&pos, 4); pos.data = (void *)(uintptr_t)0xC00000;
+    ck.type = 1; set4(ck.ne, 128, 2048, 8, 1); contig(&ck, 2); ck.data = (void *)(uintptr_t)0xD00000;
+    cv = ck; cv.data = (void *)(uintptr_t)0xE00000;
+    rid.type = 27; set4(rid.ne, 7, 1, 1, 1); contig(&rid, 8); rid.data = (void *)(uintptr_t)0xF00000;
+    qo.type = 1; set4(qo.ne, 128, 32, 7, 1); contig(&qo, 2); qo.data = (void *)(uintptr_t)0x1000000;
+    qo.src[0] = &nq; qo.src[1] = &nk; qo.src[2] = &nv; qo.src[3] = &qw; qo.src[4] = &kw;
+    qo.src[5] = &pos; qo.src[6] = &ck; qo.src[7] = &cv; qo.src[8] = &rid;
+    const mxfa_norm_rope_params np = {1e-6f, 1000000.0f, 0};
+    mxfa_tensor nt[10];
+    const mxfa_tensor *nrows = NULL;
+    printf("nr_unpack %d\n", mxfa_ggml_unpack_norm_rope(&qo, nt, &nrows));
+    show("nr_q", &nt[0]); show("nr_kcache", &nt[6]); show("nr_qout", &nt[8]); show("nr_rows", nrows);
+    printf("nr_supports %d\n", mxfa_ggml_qk_norm_rope_supports(&qo, &np));
+    pos.type = 27;   /* I64 positions: the rope positions are I32 */
+    printf("nr_bad_pos %d\n", mxfa_ggml_qk_norm_rope_supports(&qo, &np));
+    pos.type = 26;
+    qo.src[8] = NULL;   /* no row ids: row s of the caches */
+    printf("nr_no_rows %d\n", mxfa_ggml_qk_norm_rope_supports(&qo, &np));
+    qo.src[6] = NULL;
+    printf("nr_no_cache %d %d\n", mxfa_ggml_qk_norm_rope_supports(&qo, &np), mxfa_ggml_qk_norm_rope(&qo, &np, NULL));
     return 0;
 }

@@ -59,3 +59,19 @@ def test_set_rows_node(exe):
     assert o["set_rows_supports"] == "1"
     assert o["set_rows_bad_ids"] == "0"
     assert o["set_rows_no_ids"] == "0 -1"
+
+
+def test_norm_rope_node(exe):
+    """The pre-attention step as one custom node: sources in the documented
+    order, Q out as the node, row ids optional; wrong position type and a
+    missing cache source are refused without a launch."""
+    o = run(exe)
+    assert o["nr_unpack"] == "0"
+    assert o["nr_q"] == "type=0 ne=128,32,7,1 nb=4,512,16384,114688 data=0x800000"
+    assert o["nr_kcache"] == "type=1 ne=128,2048,8,1 nb=2,256,524288,4194304 data=0xd00000"
+    assert o["nr_qout"] == "type=1 ne=128,32,7,1 nb=2,256,8192,57344 data=0x1000000"
+    assert o["nr_rows"] == "type=27 ne=7,1,1,1 nb=8,56,56,56 data=0xf00000"
+    assert o["nr_supports"] == "1"
+    assert o["nr_bad_pos"] == "0"
+    assert o["nr_no_rows"] == "1"
+    assert o["nr_no_cache"] == "0 -1"
