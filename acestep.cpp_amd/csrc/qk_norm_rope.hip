@@ -38,9 +38,9 @@ constexpr int kGroups = 3;   // 16-row groups a workgroup loads before it comput
 // j of the 16 holds dims 4j..4j+3 and 64+4j..64+4j+3 (the pairs it rotates,
 // two 16-byte loads), so a wave covers 4 rows per step and the row's sum of
 // squares takes 4 cross-lane steps.  Row h = 16 g + 4 wave + lane / 16 for
-// group g.  The angles of the lane's 4 pairs depend on the token's position
-// only: their chain of multiplications and sin/cos are formed once per
-// token while the row loads are in flight.
+// group g.  The pair angles depend on the token's position only: lane l
+// forms pair l's chain of multiplications and its sin/cos once per token,
+// while the row loads are in flight, and the row lanes fetch theirs.
 template <int OT>
 __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const NormRopeArgs a) {
     // (no contraction into fma: each product and sum rounds as written)
@@ -79,16 +79,24 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const NormRopeArgs a)
         }
         const f32x4 qw0 = *(const f32x4 *)(a.q_w + 4 * j), qw1 = *(const f32x4 *)(a.q_w + 64 + 4 * j);
         const f32x4 kw0 = *(const f32x4 *)(a.k_w + 4 * j), kw1 = *(const f32x4 *)(a.k_w + 64 + 4 * j);
-        // angles of pairs 4j..4j+3: `pair` float multiplications from theta_0 = pos
-        float th[4] = {0.f, 0.f, 0.f, 0.f}, t = (float)pos;
+        // angle of pair `lane`: `lane` float multiplications from theta_0 =
+        // pos; one sincosf per lane, then lane j of each 16 fetches the
+        // values of pairs 4j..4j+3 from lanes 4j..4j+3
+        float th = 0.f, t = (float)pos;
 #pragma unroll
         for (int i = 0; i < 64; i++) {
-            th[i & 3] = (i >> 2) == j ? t : th[i & 3];
+            th = i == lane ? t : th;
             t *= a.theta_scale;
         }
+        float sn1, cs1;
+        sincosf(th, &sn1, &cs1);
         float sn[4], cs[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) sincosf(th[e], &sn[e], &cs[e]);
+        for (int e = 0; e < 4; e++) {
+            const int src = 4 * (4 * j + e);   // byte address of lane 4j + e
+            sn[e] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, sn1)));
+            cs[e] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, cs1)));
+        }
 #pragma unroll
         for (int g = 0; g < kGroups; g++) {
             if (g0 + 16 * g >= H) break;   // wave-uniform
