@@ -174,6 +174,7 @@ CASES = [
     ("lm decode batch", 4, 1, 32, 8, 4096, "per_batch"),
     ("cfg pair shared rows", 2, 7, 16, 8, 512, "shared"),
     ("dit self no rows", 2, 64, 16, 16, 64, None),
+    ("wide token, two passes", 4, 3, 64, 4, 128, "shared"),   # 72 rows per token: two 48-row passes
 ]
 
 
