@@ -173,3 +173,107 @@ def test_growth_under_capture_is_refused(mx):
         mx.flash_attn_ext(dq, dk, dv, dm, c.scale, dst=refv)
         torch.cuda.synchronize()
         assert torch.equal(out, ref)
+
+
+class FusedStep:
+    """A decode step with the pre-attention fusion: per layer one
+    mxfa_qk_norm_rope (QK-norm, RoPE, 16-bit cast, K/V written into their
+    cache row) and one attention call on the F16 Q it wrote -- the layer's
+    two launches in place of the reference's op chain
+    (src/qwen3-lm.h:418-469)."""
+
+    def __init__(self, mx, L, Nh, Nkv, max_seq, n_kv_pad, seed):
+        import torch
+
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        self.mx, self.L, self.Nh, self.Nkv, self.max_seq, self.W = mx, L, Nh, Nkv, max_seq, n_kv_pad
+        dev = "cuda"
+        H = Nh + 2 * Nkv
+        self.x = [torch.zeros(1, 1, H, D, device=dev) for _ in range(L)]
+        self.w = [(1 + 0.2 * torch.randn(2, D, generator=g)).to(dev) for _ in range(L)]
+        self.cache_k = [(torch.randn(Nkv, max_seq, D, generator=g) * 0.5).half().to(dev) for _ in range(L)]
+        self.cache_v = [(torch.randn(Nkv, max_seq, D, generator=g) * 0.5).half().to(dev) for _ in range(L)]
+        self.q16 = [torch.zeros(1, 1, Nh, D, dtype=torch.float16, device=dev) for _ in range(L)]
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.rows = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.mask = torch.zeros(1, n_kv_pad, dtype=torch.float16, device=dev)
+        self.out = [torch.zeros(1, 1, Nh, D, device=dev) for _ in range(L)]
+
+    def run(self, stream=None):
+        mx, Nh, Nkv, ms, W = self.mx, self.Nh, self.Nkv, self.max_seq, self.W
+        H = Nh + 2 * Nkv
+        V = mx.DeviceView
+        for l in range(self.L):
+            x, w, kc, vc, q16, o = self.x[l], self.w[l], self.cache_k[l], self.cache_v[l], self.q16[l], self.out[l]
+            xnb = (4, 4 * D, 4 * D * H, 4 * D * H)
+            cnb = (2, 2 * D, 2 * D * ms, 2 * D * ms * Nkv)
+            wnb = (4, 4 * D, 4 * D, 4 * D)
+            mx.qk_norm_rope(V(0, (D, Nh, 1, 1), xnb, x.data_ptr(), x),
+                            V(0, (D, Nkv, 1, 1), xnb, x.data_ptr() + 4 * D * Nh, x),
+                            V(0, (D, Nkv, 1, 1), xnb, x.data_ptr() + 4 * D * (Nh + Nkv), x),
+                            V(0, (D, 1, 1, 1), wnb, w.data_ptr(), w), V(0, (D, 1, 1, 1), wnb, w.data_ptr() + 4 * D, w),
+                            V(26, (1, 1, 1, 1), (4, 4, 4, 4), self.pos.data_ptr(), self.pos), 1e-6, 1e6,
+                            V(1, (D, Nh, 1, 1), (2, 2 * D, 2 * D * Nh, 2 * D * Nh), q16.data_ptr(), q16),
+                            V(1, (D, ms, Nkv, 1), cnb, kc.data_ptr(), kc), V(1, (D, ms, Nkv, 1), cnb, vc.data_ptr(), vc),
+                            V(27, (1, 1, 1, 1), (8, 8, 8, 8), self.rows.data_ptr(), self.rows), stream=stream)
+            mx.flash_attn_ext(V(1, (D, 1, Nh, 1), (2, 2 * D * Nh, 2 * D, 2 * D * Nh), q16.data_ptr(), q16),
+                              V(1, (D, W, Nkv, 1), cnb, kc.data_ptr(), kc), V(1, (D, W, Nkv, 1), cnb, vc.data_ptr(), vc),
+                              V(1, (W, 1, 1, 1), (2, 2 * W, 2 * W, 2 * W), self.mask.data_ptr(), self.mask),
+                              1.0 / D ** 0.5,
+                              dst=V(0, (D, Nh, 1, 1), (4, 4 * D, 4 * D * Nh, 4 * D * Nh), o.data_ptr(), o),
+                              stream=stream)
+
+    def set_inputs(self, pos, seed):
+        import torch
+
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        for l in range(self.L):
+            self.x[l].copy_(torch.randn(self.x[l].shape, generator=g) * 2)
+        self.pos.fill_(pos)
+        self.rows.fill_(pos)
+        j = torch.arange(self.W)
+        self.mask.copy_(torch.where(j <= pos, 0.0, float("-inf")).half().view(1, -1))
+
+
+def test_fused_decode_step_graph_replays_match_eager(mx):
+    """The fused decode layer (pre-attention step + attention on its F16 Q)
+    captured for 4 layers and replayed for 4 tokens, each replay equal bit
+    for bit to an eager twin, caches included."""
+    import torch
+
+    L, Nh, Nkv, max_seq, W = 4, 16, 8, 1024, 512
+    gs = FusedStep(mx, L, Nh, Nkv, max_seq, W, seed=3)
+    es = FusedStep(mx, L, Nh, Nkv, max_seq, W, seed=3)
+    base = 200
+    gs.set_inputs(base - 1, seed=77)
+    gs.run()
+    es.set_inputs(base - 1, seed=77)
+    es.run()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            gs.run(stream=s.cuda_stream)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for step in range(4):
+        pos = base + step
+        print(f"[graph fused] replay {step} at position {pos}", flush=True)
+        gs.set_inputs(pos, seed=10 + step)
+        es.set_inputs(pos, seed=10 + step)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        es.run()
+        _ = torch.randn(1 << 20, device="cuda").sum()
+        torch.cuda.synchronize()
+        for l in range(L):
+            assert torch.equal(gs.out[l], es.out[l]), (step, l)
+            assert torch.equal(gs.q16[l], es.q16[l]), (step, l)
+            assert torch.equal(gs.cache_k[l], es.cache_k[l]), (step, l)
+            assert torch.equal(gs.cache_v[l], es.cache_v[l]), (step, l)
+        assert float(gs.out[0].abs().sum()) > 0
+        # the token's cache row holds the step's K (not the warm-up's)
+        assert not torch.equal(gs.cache_k[0][:, pos], torch.zeros_like(gs.cache_k[0][:, pos]))
