@@ -64,6 +64,8 @@ DESCR.update({
     "c3m": "C3 with the per-sequence lengths as metadata (splits sized from the live lengths)",
     "c4xm": "C4 cross with the encoder padding as per-batch lengths (metadata)",
     "dstep": "Qwen3-0.6B decode token: 28 layers x (KV write of K and V + FA over a 512-key window), eager vs HIP graph replay",
+    "dstepf": "the same decode token with the pre-attention fusion: 28 layers x (QK-norm + RoPE + casts + cache rows in one "
+              "kernel, then FA on its F16 Q), eager vs HIP graph replay",
     "kw2": "KV-cache write (GGML_OP_SET_ROWS) of C2: 2048 tokens x 8 KV heads, F32 -> F16 cache [128, 2048, 8]",
     "kw3": "KV-cache write of C3: 1 token x 8 KV heads for each of 8 sets, F32 -> F16 4D cache view",
     "kw5": "KV-cache write of C2 into a Q8_0 cache: 2048 tokens x 8 KV heads, F32 -> Q8_0",
@@ -250,13 +252,16 @@ def time_norm_rope(mx, torch, steps, warmup, B=1, S=2048, Nh=32, Nkv=8, max_seq=
     return ms, (tot / n if n else None), w, n_copies
 
 
-def time_decode_step(mx, torch, steps, warmup, L=28, Nh=16, Nkv=8, max_seq=8192, W=512, pos=511):
+def time_decode_step(mx, torch, steps, warmup, L=28, Nh=16, Nkv=8, max_seq=8192, W=512, pos=511, fused=False):
     """One decode token of a Qwen3-0.6B-shaped LM through the engine: per
     layer the KV-cache write of K and V (set_rows, src/qwen3-lm.h:453-454)
     and attention over the 512-key window with its causal mask
     (:465-469).  Timed eagerly (the host issues 3 * L calls per token) and
     as one HIP graph replay per token (the reference's static decode graph,
-    src/static-graph.h)."""
+    src/static-graph.h).  fused=True: per layer the pre-attention step
+    (mxfa_qk_norm_rope: QK-norm, RoPE, casts and both cache rows from the F32
+    projections, src/qwen3-lm.h:418-454) and attention on its F16 Q, 2 * L
+    calls per token."""
     Dh = 128
     dev = "cuda"
     cache_k = [torch.zeros(Nkv, max_seq, Dh, dtype=torch.float16, device=dev) for _ in range(L)]
@@ -283,10 +288,34 @@ def time_decode_step(mx, torch, steps, warmup, L=28, Nh=16, Nkv=8, max_seq=8192,
             mx.DeviceView(0, (Dh, 1, Nh, 1), (4, 4 * Dh, 4 * Dh, 4 * Dh * Nh), qs[l].data_ptr(), qs[l]),
             mx.DeviceView(0, (Dh, Nh, 1, 1), (4, 4 * Dh, 4 * Dh * Nh, 4 * Dh * Nh), outs[l].data_ptr(), outs[l])))
     dr = mx.DeviceView(27, (1, 1, 1, 1), (8, 8, 8, 8), rows.data_ptr(), rows)
+    H = Nh + 2 * Nkv
+    xs = [torch.randn(1, 1, H, Dh, device=dev) for _ in range(L)]
+    ws = [torch.ones(2, Dh, device=dev) + 0.1 * torch.randn(2, Dh, device=dev) for _ in range(L)]
+    q16 = [torch.empty(1, 1, Nh, Dh, dtype=torch.float16, device=dev) for _ in range(L)]
+    posv = torch.full((1,), pos, dtype=torch.int32, device=dev)
+    dpos = mx.DeviceView(26, (1, 1, 1, 1), (4, 4, 4, 4), posv.data_ptr(), posv)
+    xnb = (4, 4 * Dh, 4 * Dh * H, 4 * Dh * H)
+    wnb = (4, 4 * Dh, 4 * Dh, 4 * Dh)
+    fviews = []
+    for l in range(L):
+        x, w_, qh = xs[l], ws[l], q16[l]
+        fviews.append((
+            mx.DeviceView(0, (Dh, Nh, 1, 1), xnb, x.data_ptr(), x),
+            mx.DeviceView(0, (Dh, Nkv, 1, 1), xnb, x.data_ptr() + 4 * Dh * Nh, x),
+            mx.DeviceView(0, (Dh, Nkv, 1, 1), xnb, x.data_ptr() + 4 * Dh * (Nh + Nkv), x),
+            mx.DeviceView(0, (Dh, 1, 1, 1), wnb, w_.data_ptr(), w_),
+            mx.DeviceView(0, (Dh, 1, 1, 1), wnb, w_.data_ptr() + 4 * Dh, w_),
+            mx.DeviceView(1, (Dh, Nh, 1, 1), (2, 2 * Dh, 2 * Dh * Nh, 2 * Dh * Nh), qh.data_ptr(), qh),
+            mx.DeviceView(1, (Dh, 1, Nh, 1), (2, 2 * Dh * Nh, 2 * Dh, 2 * Dh * Nh), qh.data_ptr(), qh)))
     dm = mx.DeviceView(1, (W, 1, 1, 1), (2, 2 * W, 2 * W, 2 * W), mask.data_ptr(), mask)
     scale = 1.0 / math.sqrt(Dh)
 
     def step(stream):
+        if fused:
+            for (kc, vc, kw, vw, _, _, _, o), (xq, xk, xv, wq, wk, qo, qv) in zip(views, fviews):
+                mx.qk_norm_rope(xq, xk, xv, wq, wk, dpos, 1e-6, 1e6, qo, kc, vc, dr, stream=stream)
+                mx.flash_attn_ext(qv, kw, vw, dm, scale, dst=o, stream=stream)
+            return
         for kc, vc, kw, vw, ks, vs, q, o in views:
             mx.set_rows(kc, ks, dr, stream=stream)
             mx.set_rows(vc, vs, dr, stream=stream)
@@ -320,9 +349,11 @@ def time_decode_step(mx, torch, steps, warmup, L=28, Nh=16, Nkv=8, max_seq=8192,
     step(cur)
     torch.cuda.synchronize()
     mx.timing_enable(False)
-    dev_ms = sum(mx.timing_read(f)[0] for f in ("set_rows", "fa_decode"))
+    dev_ms = sum(mx.timing_read(f)[0] for f in ("set_rows", "fa_decode", "qk_norm_rope"))
     mx.timing_reset()
-    return dict(workload=DESCR["dstep"], layers=L, launches_per_token=3 * L, eager_us=round(eager_ms * 1e3, 2),
+    name = "dstepf" if fused else "dstep"
+    return dict(workload=DESCR[name], layers=L, launches_per_token=(2 if fused else 3) * L,
+                eager_us=round(eager_ms * 1e3, 2),
                 graph_us=round(graph_ms * 1e3, 2), speedup=round(eager_ms / graph_ms, 3),
                 kernel_sum_us=round(dev_ms * 1e3, 2))
 
@@ -425,7 +456,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c2m,c3m,c4xm,c2q,kw2,kw3,kw5,nr2,dstep")
+    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c2m,c3m,c4xm,c2q,kw2,kw3,kw5,nr2,dstep,dstepf")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB copy (counter calibration under rocprofv3)")
@@ -470,8 +501,8 @@ def main():
             results[name] = summarize(name, ms, kern, w, ncp)
             log(f"[bench] {name}: {json.dumps(results[name])}")
             continue
-        if name == "dstep":
-            results[name] = time_decode_step(mxfa, torch, max(20, args.steps // 4), 5)
+        if name in ("dstep", "dstepf"):
+            results[name] = time_decode_step(mxfa, torch, max(20, args.steps // 4), 5, fused=name == "dstepf")
             log(f"[bench] {name}: {json.dumps(results[name])}")
             continue
         spec = None
