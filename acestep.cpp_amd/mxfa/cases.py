@@ -300,7 +300,18 @@ def c5(**kw) -> FaCase:
     return lm_batch_q8("c5", **kw)
 
 
-BUILDERS = {"c1": c1, "c2": c2, "c3": c3, "c4s": c4_self, "c4x": c4_cross, "c5": c5}
+def c4_self8(**kw) -> FaCase:
+    """C4 self with the real DiT's 16 / 8 heads (the config lists 16 / 16)."""
+    return dit_self("c4s8", seed=SEEDS["c4s"], Nkv=8, **kw)
+
+
+def c4_cross8(**kw) -> FaCase:
+    """C4 cross with 16 / 8 heads."""
+    return dit_cross("c4x8", seed=SEEDS["c4x"], Nkv=8, **kw)
+
+
+BUILDERS = {"c1": c1, "c2": c2, "c3": c3, "c4s": c4_self, "c4x": c4_cross, "c5": c5, "c4s8": c4_self8,
+            "c4x8": c4_cross8}
 
 
 def with_q16(case: FaCase) -> FaCase:

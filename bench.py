@@ -58,6 +58,8 @@ DESCR = {
     "c4s": "DiT self-attention: B=2 (CFG), 3000 tokens, 16/16 heads, D=128, F16 KV, no mask",
     "c4x": "DiT cross-attention: B=2, 3000 q x 256 keys, 16/16 heads, D=128, F16 KV, padding mask 0-128",
     "c5": "Qwen3-4B decode over Q8_0 KV: B=4, 32/8 heads, D=128, KV 8192",
+    "c4s8": "DiT self-attention with the real DiT's 8 KV heads: B=2, 3000 tokens, 16/8 heads, D=128, no mask",
+    "c4x8": "DiT cross-attention with 8 KV heads: B=2, 3000 q x 256 keys, 16/8 heads, padding mask 0-128",
 }
 DESCR.update({
     "c2m": "C2 with the causal mask as metadata (mxfa_flash_attn_ext_masked: no mask tensor, no classifier pass)",
@@ -73,10 +75,10 @@ DESCR.update({
            "(32 Q + 8 K + 8 V heads), Q out [128, 32, 2048], K/V into their cache rows",
     "c2q": "C2 with Q in F16 as the pre-attention step writes it (no F32 Q read, no conversion)",
 })
-BOUND = {"c1": "hbm", "c2": "mfma", "c3": "hbm", "c4s": "mfma", "c4x": "hbm", "c5": "hbm",
+BOUND = {"c1": "hbm", "c2": "mfma", "c3": "hbm", "c4s": "mfma", "c4x": "hbm", "c5": "hbm", "c4s8": "mfma", "c4x8": "hbm",
          "c2m": "mfma", "c3m": "hbm", "c4xm": "hbm", "c2q": "mfma"}
 KERNEL = {"c1": "fa_decode", "c2": "fa_prefill", "c3": "fa_decode", "c4s": "fa_prefill", "c4x": "fa_prefill",
-          "c5": "fa_decode", "c2m": "fa_prefill", "c3m": "fa_decode", "c4xm": "fa_prefill", "c2q": "fa_prefill"}
+          "c5": "fa_decode", "c4s8": "fa_prefill", "c4x8": "fa_prefill", "c2m": "fa_prefill", "c3m": "fa_decode", "c4xm": "fa_prefill", "c2q": "fa_prefill"}
 STRUCTURED = {"c2m": "c2", "c3m": "c3", "c4xm": "c4x"}   # structured-mask variant -> dense config
 
 
@@ -404,6 +406,13 @@ def cpu_baseline(case, w):
         oracle.fa_ggml(case.q, case.k, case.v, case.mask, case.scale, n_threads=n_threads)
         ts.append(time.perf_counter() - t0)
     t = statistics.median(ts)
+    # and one thread, the reference's CPU path without its thread pool
+    ts1 = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        oracle.fa_ggml(case.q, case.k, case.v, case.mask, case.scale, n_threads=1)
+        ts1.append(time.perf_counter() - t0)
+    t1 = statistics.median(ts1)
     cpu = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -416,7 +425,9 @@ def cpu_baseline(case, w):
     return dict(value=round(w["flops"] / t / 1e12, 5), unit="TFLOP/s", cores=n_threads, kind="port",
                 sample=f"full C2 workload (2048 q x 32 heads, causal) repeated for ~{CPU_SAMPLE_S:.0f} s: "
                        f"median of {len(ts)} runs, {t:.3f} s each; ggml-CPU-semantics C oracle (fp16 V "
-                       f"accumulator, AVX2 reduction order), {n_threads} threads; host CPU: {cpu}")
+                       f"accumulator, AVX2 reduction order), {n_threads} threads; host CPU: {cpu}",
+                single_thread=dict(value=round(w["flops"] / t1 / 1e12, 5), unit="TFLOP/s", cores=1,
+                                   sample=f"the same workload, median of {len(ts1)} runs, {t1:.3f} s each"))
 
 
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "fa_prefill_c2_traffic.md")
@@ -456,7 +467,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c2m,c3m,c4xm,c2q,kw2,kw3,kw5,nr2,dstep,dstepf")
+    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c4s8,c4x8,c2m,c3m,c4xm,c2q,kw2,kw3,kw5,nr2,dstep,dstepf")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB copy (counter calibration under rocprofv3)")
