@@ -243,6 +243,14 @@ __device__ void live_range(const FaArgs &a, const Tile &t, int k0, int k1, int *
     hi = last + 1;
 }
 
+// 16 bytes stored at agent scope: global_store_dwordx4 with sc1, the
+// encoding a relaxed agent-scope atomic store of each element gets on this
+// architecture (written through past the XCD's L2), in one transaction
+// instead of four.  Complete at device scope once vmcnt drains.
+__device__ __forceinline__ void st_agent16(float *p, f32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+
 __device__ __forceinline__ float ld_dev(const float *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -401,8 +409,8 @@ __device__ void finish_tile(const FaArgs &a, const Tile &t, int ns, const f32x4 
     const int64_t pr0 = ((int64_t)t.b * a.Nkv + t.kvh) * a.M + t.rt * 16;   // first row of the tile
     if (out_row) {
         float *po = a.part_o + ((pr0 + rr) * a.n_splits + t.split) * kD + dd0;
-#pragma unroll
-        for (int e = 0; e < 8; e++) __hip_atomic_store(po + e, acc[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        st_agent16(po, f32x4{acc[0], acc[1], acc[2], acc[3]});
+        st_agent16(po + 4, f32x4{acc[4], acc[5], acc[6], acc[7]});
         if (dd0 == 0) {
             float *pm = a.part_ml + ((pr0 + rr) * a.n_splits + t.split) * 2;
             __hip_atomic_store(pm, mstar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

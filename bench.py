@@ -32,6 +32,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2,c3] [--no-
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -340,9 +341,16 @@ def time_decode_step(mx, torch, steps, warmup, L=28, Nh=16, Nkv=8, max_seq=8192,
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(g, stream=s):
-            step(s.cuda_stream)
+    # no garbage collection during the capture: a collected cycle that owns
+    # device memory would be released mid-capture, which the runtime refuses
+    gc.collect()
+    gc.disable()
+    try:
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                step(s.cuda_stream)
+    finally:
+        gc.enable()
     torch.cuda.synchronize()
     graph_ms = timed(g.replay)
     # per-kernel device time of one token (HIP events on the launch stream)

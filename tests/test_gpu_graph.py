@@ -13,11 +13,27 @@ copy of the state.
 """
 from __future__ import annotations
 
+import contextlib
+import gc
+
 import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
 D = 128
+
+
+@contextlib.contextmanager
+def no_gc():
+    """No garbage collection while a stream is being captured: a collected
+    cycle that owns device tensors or graphs would release them in the
+    middle of the capture, which the runtime refuses (abort)."""
+    gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        gc.enable()
 
 
 @pytest.fixture(scope="module")
@@ -106,7 +122,7 @@ def test_decode_step_graph_replays_match_eager(mx):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
+    with no_gc(), torch.cuda.stream(s):
         with torch.cuda.graph(g, stream=s):
             graph_state.run(stream=s.cuda_stream)
     torch.cuda.current_stream().wait_stream(s)
@@ -148,19 +164,21 @@ def test_growth_under_capture_is_refused(mx):
     torch.cuda.synchronize()
     s = torch.cuda.Stream()
     g = torch.cuda.CUDAGraph()
-    raised = None
-    with torch.cuda.stream(s):
+    status, detail = None, ""
+    with no_gc(), torch.cuda.stream(s):
         with torch.cuda.graph(g, stream=s):
             try:
                 mx.flash_attn_ext(dq, dk, dv, dm, c.scale, dst=dst, stream=s.cuda_stream)
             except mx.MxfaError as e:
-                raised = e
+                # keep the status only: the exception's traceback would tie
+                # this frame (graphs, tensors) into a cycle
+                status, detail = e.status, e.detail
     torch.cuda.synchronize()
-    assert raised is not None and raised.status == mx.ERR_UNSUPPORTED, raised
-    assert "captured" in raised.detail
+    assert status == mx.ERR_UNSUPPORTED, (status, detail)
+    assert "captured" in detail
     mx.reserve(dq, dk, dv, dm, c.scale)
     g2 = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
+    with no_gc(), torch.cuda.stream(s):
         with torch.cuda.graph(g2, stream=s):
             mx.flash_attn_ext(dq, dk, dv, dm, c.scale, dst=dst, stream=s.cuda_stream)
     torch.cuda.synchronize()
@@ -173,6 +191,9 @@ def test_growth_under_capture_is_refused(mx):
         mx.flash_attn_ext(dq, dk, dv, dm, c.scale, dst=refv)
         torch.cuda.synchronize()
         assert torch.equal(out, ref)
+    del g, g2
+    torch.cuda.synchronize()
+    gc.collect()
 
 
 class FusedStep:
@@ -253,7 +274,7 @@ def test_fused_decode_step_graph_replays_match_eager(mx):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
+    with no_gc(), torch.cuda.stream(s):
         with torch.cuda.graph(g, stream=s):
             gs.run(stream=s.cuda_stream)
     torch.cuda.current_stream().wait_stream(s)
