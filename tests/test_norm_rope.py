@@ -15,6 +15,8 @@ angle); V passes through untouched or clamped.
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -146,3 +148,16 @@ def test_abi_argument_checks():
     assert call(ko=mxfa.DeviceView(1, (D, S - 1, Nkv, 1), ko.nb, ko.ptr),
                 vo=mxfa.DeviceView(1, (D, S - 1, Nkv, 1), ko.nb, ko.ptr)) == mxfa.ERR_INVALID    # too few rows
     assert call(kn=mxfa.DeviceView(0, (64, 1, 1, 1), w.nb, w.ptr)) == mxfa.ERR_INVALID
+    # rows are read in 16-byte pieces: a misaligned view is left to the op chain
+    assert call(q=mxfa.DeviceView(0, q.ne, q.nb, q.ptr + 4)) == mxfa.ERR_UNSUPPORTED
+    assert call(qn=mxfa.DeviceView(0, w.ne, w.nb, w.ptr + 4)) == mxfa.ERR_UNSUPPORTED
+    # the supports query answers without launching (descriptors only)
+    P = ctypes.POINTER(mxfa.MxfaTensor)
+    descs = [t.desc() for t in (q, k, k, w, w, pos, qo, ko, ko)]
+    prm = mxfa.MxfaNormRopeParams(EPS, BASE, 0)
+    ref = [ctypes.byref(d) for d in descs]
+    assert mxfa.lib.mxfa_qk_norm_rope_supports(ref[0], ref[1], ref[2], ref[3], ref[4], ref[5], ctypes.byref(prm),
+                                               ref[6], ref[7], ref[8], None) == 1
+    bad_pos = mxfa.DeviceView(27, pos.ne, (8, 8 * S, 8 * S, 8 * S), pos.ptr).desc()
+    assert mxfa.lib.mxfa_qk_norm_rope_supports(ref[0], ref[1], ref[2], ref[3], ref[4], ctypes.byref(bad_pos),
+                                               ctypes.byref(prm), ref[6], ref[7], ref[8], None) == 0
