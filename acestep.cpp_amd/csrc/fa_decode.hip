@@ -547,7 +547,9 @@ fa_decode_lds_kernel(const FaArgs a) {
     // scan needs anyway) does not leave the ring empty behind it.
     const int kbw_spec = k0 + 16 * t.wave;
     const int nblk_spec = kbw_spec < k1 ? (k1 - kbw_spec + 63) / 64 : 0;
-    const int n_spec = min(NST, nblk_spec);
+    // (one stage under a dense mask: a split that the scan finds wholly past
+    // its sequence's end then wastes one stage of K/V reads, not a ring)
+    const int n_spec = min(MM == kMaskVec ? 1 : NST, nblk_spec);
     for (int s = 0; s < n_spec; s++) issue(kbw_spec + 64 * s, s);
 
     int lo = k0, hi = k1;
