@@ -634,6 +634,13 @@ fa_decode_lds_kernel(const FaArgs a) {
         const u16x8 pb8 = cvt8<KT>(p, f32x4{0.f, 0.f, 0.f, 0.f});
         lsum = sum8<KT>(pb8, lsum);
         const u16x4 pb = {pb8[0], pb8[1], pb8[2], pb8[3]};
+        // bf16: the lo parts of P for a second PV product (bf16_lo)
+        u16x4 pl = {0, 0, 0, 0};
+        if constexpr (KT == T_BF16) {
+            const u16x8 pl8 = bf16_lo8(p, f32x4{0.f, 0.f, 0.f, 0.f}, pb8);
+            lsum = sum8<KT>(pl8, lsum);
+            pl = u16x4{pl8[0], pl8[1], pl8[2], pl8[3]};
+        }
 
         // O^T[d][row] += V^T[d][keys 4*g16 + e] . P^T; V values of dead
         // keys are masked to zero (operand element e <-> key 4*g16 + e)
@@ -648,6 +655,7 @@ fa_decode_lds_kernel(const FaArgs a) {
             u16x4 av = lds_read_tr16(st + kStV + tr_key * 256 + 16 * (c ^ swz_dv(tr_key)) + 8 * tr_half);
             if (any_dead) av = __builtin_bit_cast(u16x4, __builtin_bit_cast(uint64_t, av) & vmask);
             o[dt] = PV::run(av, pb, o[dt]);
+            if constexpr (KT == T_BF16) o[dt] = PV::run(av, pl, o[dt]);
         }
     };
 
@@ -901,6 +909,13 @@ fa_decode_reg_kernel(const FaArgs a) {
         const u16x8 pbits = cvt8<TV>(p0, p1);
         lsum = sum8<TV>(pbits, lsum);
         const V8 pb = __builtin_bit_cast(V8, pbits);
+        // bf16: the lo parts of P for a second PV product (bf16_lo)
+        V8 pl = {};
+        if constexpr (TV == T_BF16) {
+            const u16x8 lbits = bf16_lo8(p0, p1, pbits);
+            lsum = sum8<TV>(lbits, lsum);
+            pl = __builtin_bit_cast(V8, lbits);
+        }
 
         // V^T into this wave's LDS tile.  Chunk kc (4 keys) of row d is
         // stored at chunk slot kc ^ ((d >> 4) & 7).
@@ -943,6 +958,7 @@ fa_decode_reg_kernel(const FaArgs a) {
             u16x4 vhi = *(const u16x4 *)(row + 4 * ((g16 + 4) ^ dt));
             u16x8 av = {vlo[0], vlo[1], vlo[2], vlo[3], vhi[0], vhi[1], vhi[2], vhi[3]};
             o[dt] = MF::run(__builtin_bit_cast(V8, av), pb, o[dt]);
+            if constexpr (TV == T_BF16) o[dt] = MF::run(__builtin_bit_cast(V8, av), pl, o[dt]);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();

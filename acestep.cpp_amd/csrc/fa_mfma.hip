@@ -457,12 +457,26 @@ fa_prefill_kernel(const FaArgs a) {
     };
     // probabilities of pair u (registers 2u, 2u+1) of a half, packed into
     // the P^T operand: k-slot 4u' + i <-> key 16kk + 8u' + 4h + i =
-    // register 8kk + 4u' + i, i.e. operand kk holds registers 8kk..8kk+7
-    auto pair = [&](const f32x16 &sc, int u, float g, float mneg, u16x8 (&pw)[2]) __attribute__((always_inline)) {
+    // register 8kk + 4u' + i, i.e. operand kk holds registers 8kk..8kk+7.
+    // bf16: pl receives the lo parts (bf16_lo), which a second PV MFMA adds.
+    constexpr bool kLo = T == T_BF16;
+    auto pair = [&](const f32x16 &sc, int u, float g, float mneg, u16x8 (&pw)[2], u16x8 (&pl)[2])
+                    __attribute__((always_inline)) {
         const float p0 = fast_exp2(fmaf(sc[2 * u], g, mneg));
         const float p1 = fast_exp2(fmaf(sc[2 * u + 1], g, mneg));
-        pw[u >> 2][2 * (u & 3)] = Mfma16<T>::from_f32(p0);
-        pw[u >> 2][2 * (u & 3) + 1] = Mfma16<T>::from_f32(p1);
+        const uint16_t h0 = Mfma16<T>::from_f32(p0), h1 = Mfma16<T>::from_f32(p1);
+        pw[u >> 2][2 * (u & 3)] = h0;
+        pw[u >> 2][2 * (u & 3) + 1] = h1;
+        if constexpr (kLo) {
+            pl[u >> 2][2 * (u & 3)] = bf16_lo(p0, h0);
+            pl[u >> 2][2 * (u & 3) + 1] = bf16_lo(p1, h1);
+        }
+    };
+    // the denominator sums exactly the weights the PV product uses
+    auto psum = [&](const u16x8 (&pw)[2], const u16x8 (&pl)[2]) __attribute__((always_inline)) -> float {
+        float l = sum8<T>(pw[1], sum8<T>(pw[0], 0.0f));
+        if constexpr (kLo) l = sum8<T>(pl[1], sum8<T>(pl[0], l));
+        return l;
     };
     auto half_max = [&](const f32x16 &sc) __attribute__((always_inline)) {
         return fmaxf(fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
@@ -506,21 +520,22 @@ fa_prefill_kernel(const FaArgs a) {
         // ---- R2: QK b | softmax a (speculative) ----
         const float mneg0 = (m2 == -INFINITY) ? 0.0f : -m2;
         float mxa = 0.0f;
-        u16x8 pa[2], pb[2];
+        u16x8 pa[2], pb[2], pal[2], pbl[2];
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             if (t + 2 < 8) op[t + 2] = kread(st_c, 1, t + 2);
             else op[t - 6] = vread(st_c, 0, t - 6);   // PV a operands 0, 1
             sb = MF::run(__builtin_bit_cast(V8, op[t]), qb[t], t == 0 ? f32x16{} : sb);
             if (t == 0) mxa = half_max(sa);
-            else pair(sa, t - 1, g, mneg0, pa);
-            if (t == 7) pair(sa, 7, g, mneg0, pa);
+            else pair(sa, t - 1, g, mneg0, pa, pal);
+            if (t == 7) pair(sa, 7, g, mneg0, pa, pal);
             __builtin_amdgcn_sched_barrier(0);
         }
-        float la = sum8<T>(pa[1], sum8<T>(pa[0], 0.0f));
+        float la = psum(pa, pal);
         // keep the speculative softmax here, overlapped with QK b (it is
         // redone on the rare path, so it would otherwise sink past R3)
         asm volatile("" ::"v"(pa[0]), "v"(pa[1]), "v"(la), "v"(mxa));
+        if constexpr (kLo) asm volatile("" ::"v"(pal[0]), "v"(pal[1]));
         if (general) general_x(sb, key0 + 32);
         __builtin_amdgcn_sched_barrier(0);
 
@@ -536,8 +551,8 @@ fa_prefill_kernel(const FaArgs a) {
             for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
             const float mn = (m2 == -INFINITY) ? 0.0f : -m2;
 #pragma unroll
-            for (int u = 0; u < 8; u++) pair(sa, u, g, mn, pa);
-            la = sum8<T>(pa[1], sum8<T>(pa[0], 0.0f));
+            for (int u = 0; u < 8; u++) pair(sa, u, g, mn, pa, pal);
+            la = psum(pa, pal);
         }
         const float mneg = (m2 == -INFINITY) ? 0.0f : -m2;
         __builtin_amdgcn_sched_barrier(0);
@@ -548,10 +563,12 @@ fa_prefill_kernel(const FaArgs a) {
             if (i + 2 < 8) op[(i + 2) & 7] = vread(st_c, 0, i + 2);
             else op[(i + 2) & 7] = vread(st_c, 1, i - 6);   // PV b operands 0, 1
             o[i & 3] = MF::run(__builtin_bit_cast(V8, op[i & 7]), __builtin_bit_cast(V8, pa[i >> 2]), o[i & 3]);
-            pair(sb, i, g, mneg, pb);
+            if constexpr (kLo)
+                o[i & 3] = MF::run(__builtin_bit_cast(V8, op[i & 7]), __builtin_bit_cast(V8, pal[i >> 2]), o[i & 3]);
+            pair(sb, i, g, mneg, pb, pbl);
             __builtin_amdgcn_sched_barrier(0);
         }
-        const float lb = sum8<T>(pb[1], sum8<T>(pb[0], 0.0f));
+        const float lb = psum(pb, pbl);
         __builtin_amdgcn_sched_barrier(0);
 
         // ---- R5: PV b ----
@@ -559,6 +576,8 @@ fa_prefill_kernel(const FaArgs a) {
         for (int i = 0; i < 8; i++) {
             if (i + 2 < 8) op[(i + 2) & 7] = vread(st_c, 1, i + 2);
             o[i & 3] = MF::run(__builtin_bit_cast(V8, op[i & 7]), __builtin_bit_cast(V8, pb[i >> 2]), o[i & 3]);
+            if constexpr (kLo)
+                o[i & 3] = MF::run(__builtin_bit_cast(V8, op[i & 7]), __builtin_bit_cast(V8, pbl[i >> 2]), o[i & 3]);
             __builtin_amdgcn_sched_barrier(0);
         }
         lsum += la + lb;

@@ -8,10 +8,12 @@
 //     preceded by the mask tile classifier when a mask is given;
 // and GGML_OP_SET_ROWS, the KV-cache write before each attention node
 // (set_rows.hip).
-// The only memory the engine owns is per device and grow-only: a workspace
-// (split partials, mask tile classes) and the split tickets, freed by
-// mxfa_release().  Calls that overlap on one device (different streams)
-// share them and must be serialised by the caller.
+// The only memory the engine owns is per (device, stream) and grow-only: a
+// workspace (split partials, mask tile classes) and the split tickets.  A
+// grow retires the old buffers instead of freeing them -- kernels still
+// queued, or a HIP graph captured earlier, may hold their addresses -- and
+// mxfa_release() frees everything.  Calls on different streams use
+// different workspaces and may overlap in time.
 
 #include <hip/hip_runtime.h>
 
@@ -45,13 +47,16 @@ int fail(int code, const char *fmt, ...) {
 }
 
 struct Workspace {
+    int device = 0;
+    hipStream_t stream = nullptr;
     void *ptr = nullptr;
     size_t size = 0;
     int *tickets = nullptr;   // zero between calls
     int64_t n_tickets = 0;
+    std::vector<void *> retired;   // outgrown buffers, freed by mxfa_release()
 };
 std::mutex g_ws_mu;
-std::vector<Workspace> g_ws;  // indexed by HIP device id
+std::vector<Workspace> g_ws;  // one per (device, stream) that has needed one
 
 // Query-run length from which the MFMA prefill kernel is used.
 constexpr int64_t kPrefillMinSq = 64;
@@ -480,12 +485,20 @@ int ensure_workspace(size_t bytes, int64_t n_tickets, hipStream_t stream, void *
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return fail(MXFA_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
     std::lock_guard<std::mutex> lock(g_ws_mu);
-    if ((size_t)dev >= g_ws.size()) g_ws.resize(dev + 1);
-    Workspace &ws = g_ws[dev];
+    Workspace *found = nullptr;
+    for (Workspace &w : g_ws)
+        if (w.device == dev && w.stream == stream) found = &w;
+    if (!found) {
+        g_ws.push_back(Workspace{});
+        found = &g_ws.back();
+        found->device = dev;
+        found->stream = stream;
+    }
+    Workspace &ws = *found;
     if (ws.size < bytes || ws.n_tickets < n_tickets) {
-        // Growing allocates and synchronises, which a stream under HIP graph
-        // capture cannot do: the first call of a shape must run eagerly (or
-        // through mxfa_reserve) before a graph containing it is captured.
+        // Growing allocates, which a stream under HIP graph capture cannot
+        // do: the first call of a shape must run eagerly (or through
+        // mxfa_reserve) before a graph containing it is captured.
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
             return fail(MXFA_ERR_UNSUPPORTED,
@@ -493,44 +506,30 @@ int ensure_workspace(size_t bytes, int64_t n_tickets, hipStream_t stream, void *
                         "run the call once eagerly or call mxfa_reserve() before capture",
                         bytes, (long long)n_tickets);
     }
+    // An outgrown buffer is retired, not freed: kernels queued on the
+    // stream, and graphs captured earlier, keep using its address.
     if (ws.size < bytes) {
-        if (ws.ptr) {
-            // queued kernels may still read the old buffer
-            e = hipStreamSynchronize(stream);
-            if (e != hipSuccess) return fail(MXFA_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
-            (void)hipFree(ws.ptr);
-            ws.ptr = nullptr;
-            ws.size = 0;
-        }
         size_t want = bytes + bytes / 4;
         want = (want + 4095) & ~(size_t)4095;
-        e = hipMalloc(&ws.ptr, want);
-        if (e != hipSuccess) {
-            ws.ptr = nullptr;
-            return fail(MXFA_ERR_NOMEM, "hipMalloc(%zu): %s", want, hipGetErrorString(e));
-        }
+        void *p = nullptr;
+        e = hipMalloc(&p, want);
+        if (e != hipSuccess) return fail(MXFA_ERR_NOMEM, "hipMalloc(%zu): %s", want, hipGetErrorString(e));
+        if (ws.ptr) ws.retired.push_back(ws.ptr);
+        ws.ptr = p;
         ws.size = want;
     }
     if (ws.n_tickets < n_tickets) {
-        if (ws.tickets) {
-            e = hipStreamSynchronize(stream);
-            if (e != hipSuccess) return fail(MXFA_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
-            (void)hipFree(ws.tickets);
-            ws.tickets = nullptr;
-            ws.n_tickets = 0;
-        }
         const int64_t want = std::max<int64_t>(1024, n_tickets + n_tickets / 4);
-        e = hipMalloc((void **)&ws.tickets, (size_t)want * sizeof(int));
+        int *p = nullptr;
+        e = hipMalloc((void **)&p, (size_t)want * sizeof(int));
+        if (e != hipSuccess) return fail(MXFA_ERR_NOMEM, "hipMalloc(tickets): %s", hipGetErrorString(e));
+        e = launch_fill_zero(p, want, stream);
         if (e != hipSuccess) {
-            ws.tickets = nullptr;
-            return fail(MXFA_ERR_NOMEM, "hipMalloc(tickets): %s", hipGetErrorString(e));
-        }
-        e = launch_fill_zero(ws.tickets, want, stream);
-        if (e != hipSuccess) {
-            (void)hipFree(ws.tickets);
-            ws.tickets = nullptr;
+            (void)hipFree(p);
             return fail(MXFA_ERR_HIP, "ticket fill: %s", hipGetErrorString(e));
         }
+        if (ws.tickets) ws.retired.push_back(ws.tickets);
+        ws.tickets = p;
         ws.n_tickets = want;
     }
     *out = ws.ptr;
@@ -542,12 +541,13 @@ int ensure_workspace(size_t bytes, int64_t n_tickets, hipStream_t stream, void *
 struct TimedLaunch {
     std::string family;
     hipEvent_t start = nullptr, stop = nullptr;
+    int launches = 1;   // back-to-back launches between the two events
 };
 struct FamilyStats {
     double ms = 0.0;
     int64_t launches = 0;
 };
-std::atomic<bool> g_timing{false};
+std::atomic<int> g_timing{0};   // launches per bracket (0: timing off)
 std::mutex g_timing_mu;
 std::vector<TimedLaunch *> g_pending;
 std::vector<std::pair<std::string, FamilyStats>> g_stats;
@@ -567,7 +567,7 @@ void drain_pending() {
             hipEventElapsedTime(&ms, t->start, t->stop) == hipSuccess) {
             FamilyStats &st = stats_of(t->family);
             st.ms += ms;
-            st.launches += 1;
+            st.launches += t->launches;
         }
         if (t->start) (void)hipEventDestroy(t->start);
         if (t->stop) (void)hipEventDestroy(t->stop);
@@ -617,7 +617,7 @@ int run(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const 
 
 namespace mxfa {
 
-bool timing_enabled() { return g_timing.load(std::memory_order_relaxed); }
+int timing_mode() { return g_timing.load(std::memory_order_relaxed); }
 
 void timing_begin(const char *family, hipStream_t stream, void **token) {
     TimedLaunch *t = new TimedLaunch;
@@ -631,9 +631,10 @@ void timing_begin(const char *family, hipStream_t stream, void **token) {
     *token = t;
 }
 
-void timing_end(void *token, hipStream_t stream) {
+void timing_end(void *token, hipStream_t stream, int launches) {
     TimedLaunch *t = (TimedLaunch *)token;
     if (!t) return;
+    t->launches = launches;
     if (hipEventCreate(&t->stop) != hipSuccess || hipEventRecord(t->stop, stream) != hipSuccess) {
         if (t->stop) (void)hipEventDestroy(t->stop);
         t->stop = nullptr;
@@ -745,16 +746,28 @@ void mxfa_release(void) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
     int cur = 0;
     const bool have_cur = hipGetDevice(&cur) == hipSuccess;
-    for (size_t d = 0; d < g_ws.size(); d++) {
-        if (!g_ws[d].ptr && !g_ws[d].tickets) continue;
-        if (hipSetDevice((int)d) == hipSuccess) {
-            (void)hipDeviceSynchronize();
-            if (g_ws[d].ptr) (void)hipFree(g_ws[d].ptr);
-            if (g_ws[d].tickets) (void)hipFree(g_ws[d].tickets);
-        }
-        g_ws[d] = Workspace{};
+    for (Workspace &w : g_ws) {
+        if (hipSetDevice(w.device) != hipSuccess) continue;
+        (void)hipDeviceSynchronize();
+        if (w.ptr) (void)hipFree(w.ptr);
+        if (w.tickets) (void)hipFree(w.tickets);
+        for (void *p : w.retired) (void)hipFree(p);
     }
+    g_ws.clear();
     if (have_cur) (void)hipSetDevice(cur);
+}
+
+int mxfa_workspace_info(int64_t *live_bytes, int64_t *retired_buffers) {
+    if (!live_bytes || !retired_buffers) return fail(MXFA_ERR_INVALID, "NULL argument");
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    int64_t live = 0, ret = 0;
+    for (const Workspace &w : g_ws) {
+        live += (int64_t)w.size + w.n_tickets * (int64_t)sizeof(int);
+        ret += (int64_t)w.retired.size();
+    }
+    *live_bytes = live;
+    *retired_buffers = ret;
+    return MXFA_OK;
 }
 
 const char *mxfa_status_string(int status) {
@@ -770,7 +783,7 @@ const char *mxfa_status_string(int status) {
 
 const char *mxfa_last_error(void) { return g_last_error.c_str(); }
 
-void mxfa_timing_enable(int on) { g_timing.store(on != 0); }
+void mxfa_timing_enable(int on) { g_timing.store(on < 0 ? 0 : std::min(on, 1000)); }
 
 int mxfa_timing_read(const char *kernel, double *total_ms, int64_t *launches) {
     if (!kernel || !total_ms || !launches) return fail(MXFA_ERR_INVALID, "NULL argument");

@@ -178,6 +178,22 @@ __device__ __forceinline__ u16x8 cvt8(f32x4 lo, f32x4 hi) {
     return r;
 }
 
+// bf16 keeps 8 significant bits: a probability rounded once to bf16 for the
+// PV product is off by up to 2^-9 relative, which on short or peaked rows
+// moves the output by ~1e-3.  The bf16 kernels therefore feed the PV MFMA
+// twice, with hi = RNE_bf16(p) and lo = RNE_bf16(p - hi): hi + lo carries
+// p to ~2^-17 relative.  bf16_lo returns the raw bits of lo for the hi
+// part `h` (raw bits) of p; p - hi is exact in fp32.
+__device__ __forceinline__ uint16_t bf16_lo(float p, uint16_t h) {
+    return __builtin_bit_cast(uint16_t, (__bf16)(p - __builtin_bit_cast(float, (uint32_t)h << 16)));
+}
+__device__ __forceinline__ u16x8 bf16_lo8(f32x4 lo4, f32x4 hi4, u16x8 hi) {
+    u16x8 r;
+#pragma unroll
+    for (int i = 0; i < 8; i++) r[i] = bf16_lo(i < 4 ? lo4[i] : hi4[i - 4], hi[i]);
+    return r;
+}
+
 // Sum of 8 16-bit values of format T (the rounded probabilities that feed
 // the PV product) with v_dot2 against (1, 1): the softmax denominator then
 // sums exactly the weights the numerator uses.

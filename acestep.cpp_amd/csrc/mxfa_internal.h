@@ -71,19 +71,24 @@ struct NormRopeArgs {
 };
 hipError_t launch_qk_norm_rope(const NormRopeArgs &a, int out_type, hipStream_t stream);
 
-// Per-kernel timing: when enabled, timed_launch() brackets `launch` with
-// two events on `stream` and files them under `family`.
-bool timing_enabled();
+// Per-kernel timing: with timing mode n > 0, timed_launch() runs `launch`
+// n times back to back (every launch of the engine is idempotent: it
+// rewrites its outputs from its inputs) between two events on `stream`, and
+// files the pair under `family` as n launches.
+int timing_mode();
 void timing_begin(const char *family, hipStream_t stream, void **token);
-void timing_end(void *token, hipStream_t stream);
+void timing_end(void *token, hipStream_t stream, int launches);
 
 template <typename F>
 hipError_t timed_launch(const char *family, hipStream_t stream, F launch) {
-    if (!timing_enabled()) return launch();
+    const int n = timing_mode();
+    if (n <= 0) return launch();
     void *tok = nullptr;
     timing_begin(family, stream, &tok);
-    const hipError_t e = launch();
-    timing_end(tok, stream);
+    hipError_t e = launch();
+    int done = 1;
+    for (; done < n && e == hipSuccess; done++) e = launch();
+    timing_end(tok, stream, done);
     return e;
 }
 

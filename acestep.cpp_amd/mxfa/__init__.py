@@ -46,6 +46,7 @@ EXPORTED_SYMBOLS = (
     "mxfa_set_rows_supports",
     "mxfa_set_rows",
     "mxfa_release",
+    "mxfa_workspace_info",
     "mxfa_status_string",
     "mxfa_last_error",
     "mxfa_version",
@@ -141,6 +142,8 @@ def _load():
     L.mxfa_flash_attn_ext_masked.restype = ctypes.c_int
     L.mxfa_release.argtypes = []
     L.mxfa_release.restype = None
+    L.mxfa_workspace_info.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]
+    L.mxfa_workspace_info.restype = ctypes.c_int
     L.mxfa_status_string.argtypes = [ctypes.c_int]
     L.mxfa_status_string.restype = ctypes.c_char_p
     L.mxfa_last_error.argtypes = []
@@ -335,9 +338,23 @@ def release() -> None:
     lib.mxfa_release()
 
 
-def timing_enable(on: bool = True) -> None:
-    """Bracket every engine kernel launch with HIP events (profiling aid)."""
-    lib.mxfa_timing_enable(int(bool(on)))
+def workspace_info():
+    """(live workspace bytes, outgrown buffers kept for earlier captures)."""
+    live = ctypes.c_int64(0)
+    ret = ctypes.c_int64(0)
+    rc = lib.mxfa_workspace_info(ctypes.byref(live), ctypes.byref(ret))
+    if rc != OK:
+        raise MxfaError(rc, last_error())
+    return live.value, ret.value
+
+
+def timing_enable(on=True) -> None:
+    """Profiling aid.  on = True / 1: bracket every engine kernel launch with
+    HIP events; on = n > 1: run every launch n times back to back inside one
+    event pair (counted as n launches: the kernel's own duration, without an
+    event pair per launch); False / 0: off."""
+    n = int(on) if not isinstance(on, bool) else int(on)
+    lib.mxfa_timing_enable(max(0, n))
 
 
 def timing_read(kernel: str):

@@ -91,12 +91,14 @@ int mxfa_supports(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor 
 
 /* Execute GGML_OP_FLASH_ATTN_EXT on the current HIP device, ordered on
  * `hip_stream` (a hipStream_t; NULL = the default stream).  Asynchronous:
- * returns after the launches are queued.  The engine owns only a
- * device workspace for split-KV partials and mask tile classes; it is grown
- * on demand (a grow makes the call synchronise the stream once) and kept
- * until mxfa_release().  Calls on different streams of one device must not
- * overlap in time (they share that workspace).  Returns MXFA_OK or a
- * negative status; on failure nothing was launched. */
+ * returns after the launches are queued.  The engine owns only a device
+ * workspace per (device, stream) for split-KV partials, split tickets and
+ * mask tile classes; it is grown on demand and kept until mxfa_release().
+ * A grow retires the outgrown buffers without freeing them (work already
+ * queued, and HIP graphs captured earlier, keep valid addresses), so it
+ * never synchronises.  Calls on different streams use different workspaces
+ * and may overlap in time; calls on one stream are ordered by it.  Returns
+ * MXFA_OK or a negative status; on failure nothing was launched. */
 int mxfa_flash_attn_ext(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
                         const mxfa_tensor *mask, const mxfa_params *params, mxfa_tensor *dst,
                         void *hip_stream);
@@ -218,11 +220,14 @@ int mxfa_qk_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_ten
  * capture-safe -- kernels only, no memset, no host synchronisation, split
  * tickets reset by the kernels themselves -- except when the per-device
  * workspace has to grow: that call fails with MXFA_ERR_UNSUPPORTED while
- * `hip_stream` is being captured.  mxfa_reserve() grows the workspace for
- * the given FA call on the current device (synchronising `hip_stream` if it
- * replaces a buffer) without launching anything; so does any eager call of
- * the same shapes.  Replays reuse the workspace and must not overlap in
- * time with other mxfa calls on the device.  A structured mask's host-side
+ * `hip_stream` is being captured.  mxfa_reserve() grows the workspace of
+ * `hip_stream` on the current device for the given FA call without
+ * launching anything (beyond the one-time zero fill of a new ticket
+ * buffer); so does any eager call of the same shapes on that stream.  A
+ * graph keeps the workspace addresses of the stream it was captured on:
+ * a later grow of that workspace retires the old buffers but keeps them
+ * allocated until mxfa_release(), so the graph stays valid.  Replays must
+ * not overlap in time with other mxfa calls on the capture stream.  A structured mask's host-side
  * values (pos0, window, lengths) are captured with the launch: for values
  * that change between replays use the dense mask, which lives in device
  * memory like the reference's.  (No counterpart in ggml: a backend calls
@@ -230,8 +235,16 @@ int mxfa_qk_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_ten
 int mxfa_reserve(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
                  const mxfa_params *params, void *hip_stream);
 
-/* Free the workspaces of every device (synchronises each device first). */
+/* Free the workspaces of every device and stream, retired buffers
+ * included (synchronises each device first).  Graphs captured before the
+ * call must not be replayed after it. */
 void mxfa_release(void);
+
+/* Diagnostics (no counterpart in ggml): bytes of the live workspaces
+ * (partials, classes and tickets of every device and stream) and the number
+ * of outgrown buffers kept for earlier captures.  MXFA_OK or
+ * MXFA_ERR_INVALID. */
+int mxfa_workspace_info(int64_t *live_bytes, int64_t *retired_buffers);
 
 /* Human-readable text for a status code; last error detail for MXFA_ERR_HIP
  * and MXFA_ERR_UNSUPPORTED (thread-local). */
@@ -241,14 +254,17 @@ const char *mxfa_last_error(void);
 /* Library version: major*10000 + minor*100 + patch. */
 int mxfa_version(void);
 
-/* Per-kernel timing (a profiling aid; no counterpart in ggml).  While
- * enabled, every kernel the engine launches is bracketed by two HIP events
- * recorded on its launch stream.  mxfa_timing_read() waits for the recorded
- * events, returns the summed duration (ms) and launch count of one kernel
- * family ("fa_prefill", "mask_classify", "fa_decode", "set_rows",
- * "qk_norm_rope") since the
- * last reset, and mxfa_timing_reset() clears all counters.  Disabled by
- * default; enabling it adds two event records per launch. */
+/* Per-kernel timing (a profiling aid; no counterpart in ggml).  With
+ * mxfa_timing_enable(n), n >= 1, every kernel the engine launches is run n
+ * times back to back (each launch rewrites its outputs from its inputs, so
+ * the result is unchanged) between two HIP events recorded on its launch
+ * stream, counted as n launches: with n large the average is the kernel's
+ * own duration, with no event overhead per launch.  mxfa_timing_read()
+ * waits for the recorded events, returns the summed duration (ms) and
+ * launch count of one kernel family ("fa_prefill", "mask_classify",
+ * "fa_decode", "set_rows", "qk_norm_rope") since the last reset, and
+ * mxfa_timing_reset() clears all counters.  n = 0 (the default) turns
+ * timing off. */
 void mxfa_timing_enable(int on);
 int  mxfa_timing_read(const char *kernel, double *total_ms, int64_t *launches);
 void mxfa_timing_reset(void);

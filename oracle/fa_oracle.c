@@ -299,6 +299,47 @@ static void scale_f16_avx2(int64_t n, uint16_t *y, float v) {
     for (; i < n; i++) y[i] = ora_f2h(ora_h2f(y[i]) * v);
 }
 
+/* dot_bf16 with AVX2: the same lanes, the same mul-then-add per lane and the
+ * same reduction as dot_bf16_scalar, so the bits agree. */
+__attribute__((target("avx2,fma,f16c")))
+static float dot_bf16_avx2(int64_t n, const uint16_t *x, const uint16_t *y) {
+    __m256 c[4] = {_mm256_setzero_ps(), _mm256_setzero_ps(), _mm256_setzero_ps(), _mm256_setzero_ps()};
+    int64_t i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int j = 0; j < 4; j++) {
+            const __m256i xi = _mm256_cvtepu16_epi32(_mm_loadu_si128((const __m128i *)(x + i + 8 * j)));
+            const __m256i yi = _mm256_cvtepu16_epi32(_mm_loadu_si128((const __m128i *)(y + i + 8 * j)));
+            const __m256 p = _mm256_mul_ps(_mm256_castsi256_ps(_mm256_slli_epi32(xi, 16)),
+                                           _mm256_castsi256_ps(_mm256_slli_epi32(yi, 16)));
+            c[j] = _mm256_add_ps(p, c[j]);
+        }
+    float cl[4][8];
+    for (int j = 0; j < 4; j++) _mm256_storeu_ps(cl[j], c[j]);
+    float s[8];
+    for (int l = 0; l < 8; l++) s[l] = (cl[0][l] + cl[2][l]) + (cl[1][l] + cl[3][l]);
+    float g[4];
+    for (int l = 0; l < 4; l++) g[l] = s[l + 4] + s[l];
+    float g0 = g[0] + g[2], g1 = g[1] + g[3];
+    double sumf = (double)(g0 + g1);
+    for (; i < n; i++) sumf += (double)(ora_bf2f(x[i]) * ora_bf2f(y[i]));
+    return (float)sumf;
+}
+
+/* fp32 accumulator step y[d] = fma(v16[d], s, y[d]) for an F16 or BF16 row
+ * (the scalar form converts the row, then fmaf per element: same bits). */
+__attribute__((target("avx2,fma,f16c")))
+static void mad_f32_avx2(int64_t n, float *y, const uint16_t *x, int is_bf16, float v) {
+    const __m256 vv = _mm256_set1_ps(v);
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        const __m128i xh = _mm_loadu_si128((const __m128i *)(x + i));
+        const __m256 ax = is_bf16 ? _mm256_castsi256_ps(_mm256_slli_epi32(_mm256_cvtepu16_epi32(xh), 16))
+                                  : _mm256_cvtph_ps(xh);
+        _mm256_storeu_ps(y + i, _mm256_fmadd_ps(ax, vv, _mm256_loadu_ps(y + i)));
+    }
+    for (; i < n; i++) y[i] = fmaf(is_bf16 ? ora_bf2f(x[i]) : ora_h2f(x[i]), v, y[i]);
+}
+
 static int g_have_avx2 = -1;
 static int have_avx2(void) {
     if (g_have_avx2 < 0) {
@@ -331,6 +372,20 @@ static void mad_f16(int64_t n, uint16_t *y, const uint16_t *x, float v) {
 #endif
     mad_f16_scalar(n, y, x, v);
 }
+static float dot_bf16(int64_t n, const uint16_t *x, const uint16_t *y) {
+#if ORA_X86
+    if (use_simd()) return dot_bf16_avx2(n, x, y);
+#endif
+    return dot_bf16_scalar(n, x, y);
+}
+/* returns 1 when it handled the row (F16 / BF16 row and SIMD available) */
+static int mad_f32_row(int64_t n, float *y, const uint16_t *x, int is_bf16, float v) {
+#if ORA_X86
+    if (use_simd()) { mad_f32_avx2(n, y, x, is_bf16, v); return 1; }
+#endif
+    (void)n; (void)y; (void)x; (void)is_bf16; (void)v;
+    return 0;
+}
 static void scale_f16(int64_t n, uint16_t *y, float v) {
 #if ORA_X86
     if (use_simd()) { scale_f16_avx2(n, y, v); return; }
@@ -340,7 +395,7 @@ static void scale_f16(int64_t n, uint16_t *y, float v) {
 
 /* Exposed for tests: one dot / mad step on caller buffers. */
 float ora_dot_f16(int64_t n, const uint16_t *x, const uint16_t *y) { return dot_f16(n, x, y); }
-float ora_dot_bf16(int64_t n, const uint16_t *x, const uint16_t *y) { return dot_bf16_scalar(n, x, y); }
+float ora_dot_bf16(int64_t n, const uint16_t *x, const uint16_t *y) { return dot_bf16(n, x, y); }
 float ora_dot_q8_0(int64_t n, const uint8_t *x, const uint8_t *y) { return dot_q8_0_scalar(n, x, y); }
 void ora_mad_f16(int64_t n, uint16_t *y, const uint16_t *x, float v) { mad_f16(n, y, x, v); }
 
@@ -433,7 +488,7 @@ static void *ggml_rows(void *arg) {
             const char *kd = (const char *)k->data + ic * k->nb[1] + ik2 * k->nb[2] + ik3 * k->nb[3];
             float s;
             if (k->type == ORA_F16) s = dot_f16(DK, (const uint16_t *)kd, (const uint16_t *)Qq);
-            else if (k->type == ORA_BF16) s = dot_bf16_scalar(DK, (const uint16_t *)kd, (const uint16_t *)Qq);
+            else if (k->type == ORA_BF16) s = dot_bf16(DK, (const uint16_t *)kd, (const uint16_t *)Qq);
             else s = dot_q8_0_scalar(DK, (const uint8_t *)kd, Qq);
             s = s * scale;
             if (softcap != 0.0f) s = softcap * tanhf(s);
@@ -457,6 +512,11 @@ static void *ggml_rows(void *arg) {
                     for (int64_t d = 0; d < DV; d++) VKQ32[d] *= ms;
                 } else {
                     vs = expf(s - M);
+                }
+                if ((v->type == ORA_F16 || v->type == ORA_BF16) &&
+                    mad_f32_row(DV, VKQ32, (const uint16_t *)vd, v->type == ORA_BF16, vs)) {
+                    S = S * ms + vs;
+                    continue;
                 }
                 const float *vrow;
                 if (v->type == ORA_F16) { ora_f16_to_f32((const uint16_t *)vd, V32, DV); vrow = V32; }
@@ -549,6 +609,12 @@ static void *exact_rows(void *arg) {
     double *sc = (double *)malloc(sizeof(double) * (size_t)nek1);
     float *tmp = (float *)malloc(sizeof(float) * (size_t)(DK > DV ? DK : DV));
     uint8_t *qq = (uint8_t *)malloc((size_t)DK * 4 + 64);
+    /* fp64 copies of the K and V rows of the (kv head, kv batch) plane the
+     * current row reads; rows go to threads in contiguous runs, so a plane
+     * is converted once per run instead of once per query row */
+    double *kpl = (double *)malloc(sizeof(double) * (size_t)(nek1 * DK));
+    double *vpl = (double *)malloc(sizeof(double) * (size_t)(nek1 * DV));
+    int64_t k_plane = -1, v_plane = -1;
     const int64_t dr = (J->nrows + J->nth - 1) / J->nth;
     const int64_t ir0 = dr * J->ith;
     const int64_t ir1 = ir0 + dr < J->nrows ? ir0 + dr : J->nrows;
@@ -558,6 +624,21 @@ static void *exact_rows(void *arg) {
         const int64_t iq2 = (ir - iq3 * neq2 * neq1) / neq1;
         const int64_t iq1 = ir - iq3 * neq2 * neq1 - iq2 * neq1;
         const uint32_t h = (uint32_t)iq2;
+        {
+            const int64_t kp = (iq3 / rk3) * k->ne[2] + iq2 / rk2, vp = (iq3 / rv3) * v->ne[2] + iq2 / rv2;
+            if (kp != k_plane) {
+                for (int64_t ic = 0; ic < nek1; ic++)
+                    load_row_f64(k, (const char *)k->data + ic * k->nb[1] + (iq2 / rk2) * k->nb[2] +
+                                        (iq3 / rk3) * k->nb[3], DK, kpl + ic * DK, tmp);
+                k_plane = kp;
+            }
+            if (vp != v_plane) {
+                for (int64_t ic = 0; ic < nek1; ic++)
+                    load_row_f64(v, (const char *)v->data + ic * v->nb[1] + (iq2 / rv2) * v->nb[2] +
+                                        (iq3 / rv3) * v->nb[3], DV, vpl + ic * DV, tmp);
+                v_plane = vp;
+            }
+        }
         const double slope = (J->max_bias > 0.0)
             ? (h < n_head_log2 ? pow(m0, h + 1) : pow(m1, 2 * (h - n_head_log2) + 1)) : 1.0;
         const float *pq = (const float *)((const char *)q->data + iq1 * q->nb[1] + iq2 * q->nb[2] + iq3 * q->nb[3]);
@@ -576,15 +657,13 @@ static void *exact_rows(void *arg) {
             ? (const uint16_t *)((const char *)mask->data + iq1 * mask->nb[1] +
                                  (iq2 % mask->ne[2]) * mask->nb[2] + (iq3 % mask->ne[3]) * mask->nb[3])
             : NULL;
-        const int64_t ik3 = iq3 / rk3, ik2 = iq2 / rk2, iv3 = iq3 / rv3, iv2 = iq2 / rv2;
         double M = -INFINITY;
         for (int64_t ic = 0; ic < nek1; ic++) {
             double mv = mp ? slope * (double)ora_h2f(mp[ic]) : 0.0;
             if (mv == -INFINITY) { sc[ic] = -INFINITY; continue; }
-            const char *kp = (const char *)k->data + ic * k->nb[1] + ik2 * k->nb[2] + ik3 * k->nb[3];
-            load_row_f64(k, kp, DK, kd, tmp);
+            const double *kr = kpl + ic * DK;
             double s = 0.0;
-            for (int64_t i = 0; i < DK; i++) s += kd[i] * qd[i];
+            for (int64_t i = 0; i < DK; i++) s += kr[i] * qd[i];
             s *= scale;
             if (J->softcap != 0.0) s = J->softcap * tanh(s);
             s += mv;
@@ -597,16 +676,15 @@ static void *exact_rows(void *arg) {
             for (int64_t ic = 0; ic < nek1; ic++) {
                 if (sc[ic] == -INFINITY) continue;
                 const double p = exp(sc[ic] - M);
-                const char *vp = (const char *)v->data + ic * v->nb[1] + iv2 * v->nb[2] + iv3 * v->nb[3];
-                load_row_f64(v, vp, DV, vd, tmp);
-                for (int64_t d = 0; d < DV; d++) acc[d] += p * vd[d];
+                const double *vr = vpl + ic * DV;
+                for (int64_t d = 0; d < DV; d++) acc[d] += p * vr[d];
                 S += p;
             }
         }
         double *out = J->dst + ((iq3 * neq1 + iq1) * neq2 + iq2) * DV;
         for (int64_t d = 0; d < DV; d++) out[d] = S == 0.0 ? 0.0 : acc[d] / S;
     }
-    free(qd); free(kd); free(vd); free(acc); free(sc); free(tmp); free(qq);
+    free(qd); free(kd); free(vd); free(acc); free(sc); free(tmp); free(qq); free(kpl); free(vpl);
     return NULL;
 }
 

@@ -89,7 +89,7 @@ def test_gpu_matches_fixture(path):
                             c.softcap)
     torch.cuda.synchronize()
     got = mxfa.output_tensor(o).cpu().numpy()
-    tol = 1e-2 if spec["kv_type"] == 30 else MAX_ABS_TOL
+    tol = MAX_ABS_TOL
     for ref in ("out_gate", "out_exact"):
         m = row_metrics(got, out[ref])
         assert m["max_abs"] <= tol and m["min_cos"] >= ROW_COS_TOL, (spec["name"], ref, m)

@@ -112,15 +112,17 @@ def test_decode_step_graph_replays_match_eager(mx):
     graph_state = Step(mx, L, Nh, Nkv, max_seq, W, seed=1)
     eager_state = Step(mx, L, Nh, Nkv, max_seq, W, seed=1)
     base = 300
-    # eager warm-up of the graph's own buffers sizes the engine's workspace
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    # eager warm-up of the graph's own buffers on the capture stream sizes
+    # that stream's workspace (the engine keeps one per stream)
     graph_state.set_inputs(base - 1, seed=99)
-    graph_state.run()
+    with torch.cuda.stream(s):
+        graph_state.run(stream=s.cuda_stream)
     eager_state.set_inputs(base - 1, seed=99)
     eager_state.run()
     torch.cuda.synchronize()
 
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
     g = torch.cuda.CUDAGraph()
     with no_gc(), torch.cuda.stream(s):
         with torch.cuda.graph(g, stream=s):
@@ -176,7 +178,7 @@ def test_growth_under_capture_is_refused(mx):
     torch.cuda.synchronize()
     assert status == mx.ERR_UNSUPPORTED, (status, detail)
     assert "captured" in detail
-    mx.reserve(dq, dk, dv, dm, c.scale)
+    mx.reserve(dq, dk, dv, dm, c.scale, stream=s.cuda_stream)
     g2 = torch.cuda.CUDAGraph()
     with no_gc(), torch.cuda.stream(s):
         with torch.cuda.graph(g2, stream=s):
@@ -189,6 +191,29 @@ def test_growth_under_capture_is_refused(mx):
         g2.replay()
         torch.cuda.synchronize()
         mx.flash_attn_ext(dq, dk, dv, dm, c.scale, dst=refv)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+
+    # A larger eager call on the capture stream grows its workspace after
+    # the capture: the outgrown buffers the graph holds are retired, not
+    # freed, so the graph still replays correctly (interleaved with the
+    # grown workspace's own calls).
+    _, retired0 = mx.workspace_info()
+    big = C.lm_batch("t2", N=16, Nh=32, Nkv=8, max_seq=8192, lmin=7000, lmax=8192)
+    bq, bk, bv, bm = mx.upload(big.q), mx.upload(big.k), mx.upload(big.v), mx.upload(big.mask)
+    Bb, Sqb, Nhb, DVb = big.out_shape
+    bout = torch.zeros(Bb, Sqb, Nhb, DVb, device="cuda")
+    bdst = mx.DeviceView(0, (DVb, Nhb, Sqb, Bb), (4, 4 * DVb, 4 * DVb * Nhb, 4 * DVb * Nhb * Sqb), bout.data_ptr(), bout)
+    with torch.cuda.stream(s):
+        mx.flash_attn_ext(bq, bk, bv, bm, big.scale, dst=bdst, stream=s.cuda_stream)
+    torch.cuda.synchronize()
+    live, retired1 = mx.workspace_info()
+    assert retired1 > retired0, (retired0, retired1, live)
+    for _ in range(2):
+        out.zero_()
+        with torch.cuda.stream(s):
+            g2.replay()
+            mx.flash_attn_ext(bq, bk, bv, bm, big.scale, dst=bdst, stream=s.cuda_stream)
         torch.cuda.synchronize()
         assert torch.equal(out, ref)
     del g, g2
@@ -266,13 +291,14 @@ def test_fused_decode_step_graph_replays_match_eager(mx):
     gs = FusedStep(mx, L, Nh, Nkv, max_seq, W, seed=3)
     es = FusedStep(mx, L, Nh, Nkv, max_seq, W, seed=3)
     base = 200
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
     gs.set_inputs(base - 1, seed=77)
-    gs.run()
+    with torch.cuda.stream(s):
+        gs.run(stream=s.cuda_stream)     # sizes the capture stream's workspace
     es.set_inputs(base - 1, seed=77)
     es.run()
     torch.cuda.synchronize()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
     g = torch.cuda.CUDAGraph()
     with no_gc(), torch.cuda.stream(s):
         with torch.cuda.graph(g, stream=s):

@@ -347,7 +347,7 @@ def _pipeline(mx, L, n_kv_pad, spec, label):
     ref = oracle.fa_ggml(case.q, case.k, case.v, case.mask, case.scale, acc_f32=True)
     m = row_metrics(got, ref)
     print(f"[pipeline] {label}: max_abs={m['max_abs']:.3e} min_cos={m['min_cos']:.7f}", flush=True)
-    tol = 1e-2 if ot == C.TYPE_BF16 else MAX_ABS_TOL
+    tol = MAX_ABS_TOL
     assert m["max_abs"] <= tol and m["min_cos"] >= ROW_COS_TOL, (label, m)
 
 

@@ -4,7 +4,8 @@ The reference has no flash_attn_ext golden vectors (every committed log ran
 with FA disabled, reference tests/debug-dit-cossim.py:147) and ggml itself is
 absent (empty submodule), so the oracle is pinned by:
   * library routines: numpy float16 (IEEE RNE) for the fp16 codec, torch
-    bfloat16 for the bf16 codec, published Philox KAT vectors for the RNG;
+    bfloat16 for the bf16 codec (the RNG's published Philox KAT vectors are
+    checked in tests/test_synth.py);
   * an independent numpy fp64 implementation in matrix form (the reference's
     own non-FA statement of the op: qwen3-enc.h:101-112 / dit-graph.h:123-134
     and the PyTorch restatement tests/debug-lm-logits.py:100-115) that reads
@@ -394,13 +395,18 @@ def test_simd_and_scalar_forms_agree(oracle_lib):
     q, k, v = _small_case(rng, 2, 6, 4, 2, 300)
     allowed = rng.random((2, 1, 6, 300)) > 0.2
     m = mask_view(allowed)
-    a = oracle_lib.fa_ggml(q, k, v, m, 0.088)
-    L.ora_set_force_scalar(1)
-    try:
-        b = oracle_lib.fa_ggml(q, k, v, m, 0.088)
-    finally:
-        L.ora_set_force_scalar(0)
-    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    cases = [(q, k, v)]
+    kb = _small_case(np.random.default_rng(26), 2, 6, 4, 2, 300, kv_type=BF16)
+    cases.append(kb)
+    for qq, kk, vv in cases:
+        for acc in (False, True):
+            a = oracle_lib.fa_ggml(qq, kk, vv, m, 0.088, acc_f32=acc)
+            L.ora_set_force_scalar(1)
+            try:
+                b = oracle_lib.fa_ggml(qq, kk, vv, m, 0.088, acc_f32=acc)
+            finally:
+                L.ora_set_force_scalar(0)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (kk.type, acc)
 
 
 def test_ggml_semantics_fp16_accumulation_is_visible(oracle_lib):
