@@ -118,6 +118,13 @@ class MxfaError(RuntimeError):
 def _load():
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"libmxfa.so not built: {LIB_PATH} (run `make -C acestep.cpp_amd`)")
+    # torch ships its own HIP runtime (torch/lib/libamdhip64.so, soname
+    # libamdhip64.so.7) and loads it by path.  It must be in the process
+    # before libmxfa.so, whose libamdhip64.so.7 dependency then resolves to
+    # it: loaded the other way round, the process ends up with two HIP
+    # runtimes (ROCm's and torch's) and torch's device calls crash.
+    import torch  # noqa: F401
+
     L = ctypes.CDLL(LIB_PATH)
     P = ctypes.POINTER(MxfaTensor)
     L.mxfa_supports.argtypes = [P, P, P, P, ctypes.POINTER(MxfaParams), P]

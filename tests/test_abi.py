@@ -78,3 +78,18 @@ def test_supports_rejections():
     assert not mxfa.supports(q, k, v, m, c.scale, dst=dst_bad)         # non-contiguous dst
     dst_ok = mxfa.DeviceView(0, (128, 16, 1, 1), (4, 512, 8192, 8192), 1 << 21)
     assert mxfa.supports(q, k, v, m, c.scale, dst=dst_ok)
+
+
+def test_one_hip_runtime_whatever_the_import_order():
+    """torch bundles its own HIP runtime; libmxfa.so must bind to that one
+    even when mxfa is imported before torch (two runtimes in one process
+    crash torch's device calls)."""
+    import subprocess
+    import sys
+
+    code = ("import sys, re; sys.path.insert(0, {pkg!r}); import mxfa, torch; "
+            "print(len(set(re.findall(r'\\S*libamdhip64\\S*', open('/proc/self/maps').read()))))")
+    out = subprocess.run([sys.executable, "-c", code.format(pkg=os.path.join(REPO, "acestep.cpp_amd"))],
+                         capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr[-2000:]
+    assert out.stdout.strip().splitlines()[-1] == "1", out.stdout
