@@ -163,8 +163,8 @@ int check_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tenso
                     const mxfa_tensor *kw, const mxfa_tensor *pos, const mxfa_norm_rope_params *p,
                     const mxfa_tensor *qo, const mxfa_tensor *ko, const mxfa_tensor *vo, const mxfa_tensor *rows,
                     NormRopeArgs *a, int *out_type) {
-    if (!q || !k || !v || !qw || !kw || !pos || !p || !qo || !ko || !vo)
-        return fail(MXFA_ERR_INVALID, "q, k, v, norms, positions, params and outputs are required");
+    if (!q || !k || !v || !qw || !kw || !p || !qo || !ko || !vo)
+        return fail(MXFA_ERR_INVALID, "q, k, v, norms, params and outputs are required");
     for (const mxfa_tensor *t : {q, k, v, qw, kw, pos, qo, ko, vo, rows}) {
         if (!t) continue;
         for (int i = 0; i < 4; i++)
@@ -175,17 +175,19 @@ int check_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tenso
         if (t->type != MXFA_TYPE_F32 || t->ne[0] != kD || t->nb[0] != 4 || !is_aligned(t->data, 16) ||
             t->nb[1] % 16 || t->nb[2] % 16 || t->nb[3] % 16)
             return fail(MXFA_ERR_UNSUPPORTED, "q/k/v must be F32 rows of 128 values, 16-byte aligned");
-    const int64_t Nh = q->ne[1], Nkv = k->ne[1], S = q->ne[2], B = q->ne[3];
-    if (v->ne[1] != Nkv || k->ne[2] != S || v->ne[2] != S || k->ne[3] != B || v->ne[3] != B)
+    // positions == NULL: no RoPE (DiT cross-attention); K/V may then have
+    // their own token count
+    const int64_t Nh = q->ne[1], Nkv = k->ne[1], S = q->ne[2], B = q->ne[3], Skv = k->ne[2];
+    if (v->ne[1] != Nkv || v->ne[2] != Skv || k->ne[3] != B || v->ne[3] != B || (pos && Skv != S))
         return fail(MXFA_ERR_INVALID, "q/k/v shapes disagree");
     for (const mxfa_tensor *t : {qw, kw})
         if (t->type != MXFA_TYPE_F32 || t->ne[0] != kD || t->ne[1] * t->ne[2] * t->ne[3] != 1 || t->nb[0] != 4)
             return fail(MXFA_ERR_INVALID, "norm weights must be F32 [128]");
     for (const mxfa_tensor *t : {qw, kw})
         if (!is_aligned(t->data, 16)) return fail(MXFA_ERR_UNSUPPORTED, "norm weights must be 16-byte aligned");
-    if (pos->type != MXFA_TYPE_I32 || pos->ne[0] != S || (pos->ne[1] != 1 && pos->ne[1] != B) || pos->ne[2] != 1 ||
-        pos->ne[3] != 1 || pos->nb[0] != 4 || (pos->ne[1] > 1 && pos->nb[1] != 4 * (size_t)S) ||
-        !is_aligned(pos->data, 4))
+    if (pos && (pos->type != MXFA_TYPE_I32 || pos->ne[0] != S || (pos->ne[1] != 1 && pos->ne[1] != B) ||
+                pos->ne[2] != 1 || pos->ne[3] != 1 || pos->nb[0] != 4 ||
+                (pos->ne[1] > 1 && pos->nb[1] != 4 * (size_t)S) || !is_aligned(pos->data, 4)))
         return fail(MXFA_ERR_INVALID, "positions must be I32 [S] or [S, B], contiguous");
     const int ot = qo->type;
     if (ot != MXFA_TYPE_F16 && ot != MXFA_TYPE_BF16)
@@ -202,16 +204,17 @@ int check_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tenso
         return fail(MXFA_ERR_INVALID, "k_out and v_out layouts differ");
     if (rows) {
         const size_t es = rows->type == MXFA_TYPE_I64 ? 8 : 4;
-        if ((rows->type != MXFA_TYPE_I64 && rows->type != MXFA_TYPE_I32) || rows->ne[0] != S || B % rows->ne[1] ||
+        if ((rows->type != MXFA_TYPE_I64 && rows->type != MXFA_TYPE_I32) || rows->ne[0] != Skv || B % rows->ne[1] ||
             rows->ne[2] != 1 || rows->ne[3] != 1 || rows->nb[0] != es || !is_aligned(rows->data, es) ||
             rows->nb[1] % es)
-            return fail(MXFA_ERR_INVALID, "rows must be I64/I32 [S, R] with B %% R == 0");
-    } else if (ko->ne[1] < S) {
-        return fail(MXFA_ERR_INVALID, "without rows, k_out/v_out need at least S rows");
+            return fail(MXFA_ERR_INVALID, "rows must be I64/I32 [Skv, R] with B %% R == 0");
+    } else if (ko->ne[1] < Skv) {
+        return fail(MXFA_ERR_INVALID, "without rows, k_out/v_out need at least one row per K/V token");
     }
     if (!(p->eps >= 0.0f) || !std::isfinite(p->eps) || !(p->freq_base > 0.0f) || !std::isfinite(p->freq_base))
         return fail(MXFA_ERR_INVALID, "eps / freq_base invalid");
-    if ((Nh + 2 * Nkv) * S * B >= ((int64_t)1 << 40) || S * B >= ((int64_t)1 << 31) || Nh + 2 * Nkv > 4096)
+    if ((Nh + 2 * Nkv) * std::max(S, Skv) * B >= ((int64_t)1 << 40) || std::max(S, Skv) * B >= ((int64_t)1 << 31) ||
+        Nh + 2 * Nkv > 4096)
         return fail(MXFA_ERR_UNSUPPORTED, "too many rows");
     if (a) {
         NormRopeArgs &r = *a;
@@ -226,8 +229,10 @@ int check_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tenso
         }
         r.q_w = (const float *)qw->data;
         r.k_w = (const float *)kw->data;
-        r.pos = (const int32_t *)pos->data;
-        r.pos_per_batch = pos->ne[1] > 1;
+        r.pos = pos ? (const int32_t *)pos->data : nullptr;
+        r.pos_per_batch = pos && pos->ne[1] > 1;
+        r.rope = pos != nullptr;
+        r.Skv = (int32_t)Skv;
         r.eps = p->eps;
         r.theta_scale = std::pow(p->freq_base, -2.0f / (float)kD);
         r.clamp_v = p->clamp_v != 0;

@@ -51,9 +51,11 @@ struct SetRowsArgs {
 hipError_t launch_set_rows(const SetRowsArgs &a, int dtype, hipStream_t stream);
 
 // Pre-attention fusion (QK-RMSNorm, NEOX RoPE, 16-bit cast, KV-cache
-// write); see qk_norm_rope.hip.  Q/K/V rows are F32 [128, H, S, B] with
-// strides {head, token, batch}; Q goes to [128, Nh, S, B] contiguous, K/V to
-// row rows[s, b % r_ne1] (or s) of their [128, kv_rows, Nkv, B] views.
+// write); see qk_norm_rope.hip.  Q/K/V rows are F32 [128, H, S | Skv, B]
+// with strides {head, token, batch}; Q goes to [128, Nh, S, B] contiguous,
+// K/V to row rows[s, b % r_ne1] (or s) of their [128, kv_rows, Nkv, B]
+// views.  rope == 0: no rotation (pos unused) and K/V may have Skv != S
+// tokens (cross-attention); with RoPE, Skv == S.
 struct NormRopeArgs {
     const char *q, *k, *v;
     int64_t q_nb[3], k_nb[3], v_nb[3];
@@ -68,6 +70,7 @@ struct NormRopeArgs {
     int64_t r_nb0, r_nb1;
     int32_t r_ne1, rows_i64;
     int32_t Nh, Nkv, S, B;
+    int32_t Skv, rope;
 };
 hipError_t launch_qk_norm_rope(const NormRopeArgs &a, int out_type, hipStream_t stream);
 

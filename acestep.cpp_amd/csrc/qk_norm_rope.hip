@@ -12,6 +12,11 @@
 // Q into [D, Nh, S, B] (attention takes its permuted view, as the reference
 // does), K and V straight into their cache rows.
 //
+// DiT cross-attention (src/dit-graph.h:317-346) runs the same chain without
+// RoPE ("no RoPE for cross-attention", :333) and with K/V from the encoder:
+// positions == NULL switches the rotation off, and K/V then have their own
+// token count Skv (enc_S) next to Q's S.
+//
 // Arithmetic as ggml's CPU ops do it:
 //   rms_norm: sum of x*x (float products) accumulated in double, mean =
 //     sum / 128, scale = 1 / sqrtf(mean + eps), y = x * scale, then * w;
@@ -47,17 +52,20 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const NormRopeArgs a)
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, sub = lane >> 4;
-    const int s = (int)(blockIdx.x % (unsigned)a.S), b = (int)(blockIdx.x / (unsigned)a.S);
+    // token s of batch b: its Q rows (s < S) and its K/V rows (s < Skv)
+    const int T = a.S > a.Skv ? a.S : a.Skv;
+    const int s = (int)(blockIdx.x % (unsigned)T), b = (int)(blockIdx.x / (unsigned)T);
     const int H = a.Nh + 2 * a.Nkv;
+    const bool q_on = s < a.S, kv_on = s < a.Skv;
 
     // K/V destination row of this token (uniform); out of range: skipped
     int64_t r = s;
-    if (a.rows) {
+    if (a.rows && kv_on) {
         const char *ip = a.rows + (int64_t)s * a.r_nb0 + (int64_t)(b % a.r_ne1) * a.r_nb1;
         r = a.rows_i64 ? *(const int64_t *)ip : (int64_t)*(const int32_t *)ip;
     }
-    const bool kv_ok = r >= 0 && r < a.kv_rows;
-    const int pos = a.pos[s + (int64_t)(a.pos_per_batch ? b : 0) * a.S];
+    const bool kv_ok = kv_on && r >= 0 && r < a.kv_rows;
+    const int pos = a.rope ? a.pos[s + (int64_t)(a.pos_per_batch ? b : 0) * a.S] : 0;
 
     for (int g0 = 0; g0 < H; g0 += 16 * kGroups) {
         f32x4 lo[kGroups], hi[kGroups];
@@ -66,7 +74,7 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const NormRopeArgs a)
         for (int g = 0; g < kGroups; g++) {
             const int h = g0 + 16 * g + 4 * wave + sub;
             lo[g] = hi[g] = f32x4{0.f, 0.f, 0.f, 0.f};
-            kind[g] = h < a.Nh ? 0 : (h < a.Nh + a.Nkv ? 1 : (h < H ? 2 : 3));
+            kind[g] = h < a.Nh ? (q_on ? 0 : 3) : (h < H ? (kv_on ? (h < a.Nh + a.Nkv ? 1 : 2) : 3) : 3);
             hh[g] = kind[g] == 0 ? h : (kind[g] == 1 ? h - a.Nh : h - a.Nh - a.Nkv);
             if (kind[g] < 3) {
                 const char *src = kind[g] == 0 ? a.q : (kind[g] == 1 ? a.k : a.v);
@@ -82,20 +90,22 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const NormRopeArgs a)
         // angle of pair `lane`: `lane` float multiplications from theta_0 =
         // pos; one sincosf per lane, then lane j of each 16 fetches the
         // values of pairs 4j..4j+3 from lanes 4j..4j+3
-        float th = 0.f, t = (float)pos;
+        float sn[4] = {0.f, 0.f, 0.f, 0.f}, cs[4] = {1.f, 1.f, 1.f, 1.f};
+        if (a.rope) {
+            float th = 0.f, t = (float)pos;
 #pragma unroll
-        for (int i = 0; i < 64; i++) {
-            th = i == lane ? t : th;
-            t *= a.theta_scale;
-        }
-        float sn1, cs1;
-        sincosf(th, &sn1, &cs1);
-        float sn[4], cs[4];
+            for (int i = 0; i < 64; i++) {
+                th = i == lane ? t : th;
+                t *= a.theta_scale;
+            }
+            float sn1, cs1;
+            sincosf(th, &sn1, &cs1);
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int src = 4 * (4 * j + e);   // byte address of lane 4j + e
-            sn[e] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, sn1)));
-            cs[e] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, cs1)));
+            for (int e = 0; e < 4; e++) {
+                const int src = 4 * (4 * j + e);   // byte address of lane 4j + e
+                sn[e] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, sn1)));
+                cs[e] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, cs1)));
+            }
         }
 #pragma unroll
         for (int g = 0; g < kGroups; g++) {
@@ -120,8 +130,13 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const NormRopeArgs a)
                 for (int e = 0; e < 4; e++) {
                     const float w0 = kd == 0 ? qw0[e] : kw0[e], w1 = kd == 0 ? qw1[e] : kw1[e];
                     const float u0 = (y0[e] * scale) * w0, u1 = (y1[e] * scale) * w1;
-                    y0[e] = u0 * cs[e] - u1 * sn[e];
-                    y1[e] = u0 * sn[e] + u1 * cs[e];
+                    if (a.rope) {
+                        y0[e] = u0 * cs[e] - u1 * sn[e];
+                        y1[e] = u0 * sn[e] + u1 * cs[e];
+                    } else {
+                        y0[e] = u0;
+                        y1[e] = u1;
+                    }
                 }
             } else if (a.clamp_v) {
 #pragma unroll
@@ -148,7 +163,7 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const NormRopeArgs a)
 }
 
 hipError_t launch_qk_norm_rope(const NormRopeArgs &a, int out_type, hipStream_t stream) {
-    const int64_t tokens = (int64_t)a.S * a.B;
+    const int64_t tokens = (int64_t)(a.S > a.Skv ? a.S : a.Skv) * a.B;
     if (tokens <= 0) return hipSuccess;
     const dim3 grid((unsigned)tokens);
     if (out_type == T_F16) hipLaunchKernelGGL(qk_norm_rope_kernel<T_F16>, grid, dim3(256), 0, stream, a);

@@ -252,16 +252,18 @@ def qk_norm_rope(q, k, v, q_norm, k_norm, positions, eps, freq_base, q_out, k_ou
                  clamp_v=False, stream: Optional[int] = None) -> None:
     """The pre-attention work of a layer in one kernel (mxfa_qk_norm_rope):
     QK-RMSNorm, NEOX RoPE, 16-bit cast of Q/K/V, K/V written into their
-    cache rows.  All arguments are DeviceViews (rows may be None)."""
+    cache rows.  All arguments are DeviceViews (rows may be None).
+    positions=None: no RoPE (DiT cross-attention), and k/v may hold their
+    own number of tokens."""
     import torch
 
     if stream is None:
         stream = torch.cuda.current_stream().cuda_stream
-    ds = [t.desc() for t in (q, k, v, q_norm, k_norm, positions, q_out, k_out, v_out)]
+    ds = [t.desc() if t is not None else None for t in (q, k, v, q_norm, k_norm, positions, q_out, k_out, v_out)]
     dr = rows.desc() if rows is not None else None
     p = MxfaNormRopeParams()
     p.eps, p.freq_base, p.clamp_v = float(eps), float(freq_base), int(bool(clamp_v))
-    refs = [ctypes.byref(d) for d in ds]
+    refs = [ctypes.byref(d) if d is not None else None for d in ds]
     rc = lib.mxfa_qk_norm_rope(refs[0], refs[1], refs[2], refs[3], refs[4], refs[5], ctypes.byref(p), refs[6],
                                refs[7], refs[8], ctypes.byref(dr) if dr is not None else None,
                                ctypes.c_void_p(int(stream)))

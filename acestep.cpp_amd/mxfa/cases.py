@@ -324,12 +324,18 @@ def with_q16(case: FaCase) -> FaCase:
     return FaCase(case.name, q, case.k, case.v, case.mask, case.scale, case.max_bias, case.softcap, dict(case.meta))
 
 
-def norm_rope_work(B: int, S: int, Nh: int, Nkv: int, rows_i64: bool = True) -> dict:
+def norm_rope_work(B: int, S: int, Nh: int, Nkv: int, rows_i64: bool = True, Skv: Optional[int] = None) -> dict:
     """Algorithmic bytes of one fused pre-attention call (mxfa_qk_norm_rope):
     every F32 row of Q, K and V read once, its 16-bit row written once, the
     positions and row ids read once (the two 512 B weights are noise).  The
     reference's op chain (rms_norm, mul, rope, cont, clamp, set_rows, and
-    attention's F32 Q read) moves several times that."""
+    attention's F32 Q read) moves several times that.  Skv given: the
+    cross-attention form (no RoPE, no positions or row ids, Skv K/V
+    tokens)."""
+    if Skv is not None:
+        n = (Nh * S + 2 * Nkv * Skv) * B
+        rd, wr = n * 4 * D, n * 2 * D
+        return dict(rows=n, read_bytes=rd, write_bytes=wr, id_bytes=0, bytes=rd + wr)
     n = (Nh + 2 * Nkv) * S * B
     rd, wr = n * 4 * D, n * 2 * D
     ids = S * B * 4 + S * B * (8 if rows_i64 else 4)

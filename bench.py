@@ -78,11 +78,15 @@ DESCR.update({
     "nr2": "pre-attention step of C2 (mxfa_qk_norm_rope): QK-RMSNorm + NEOX RoPE + F16 cast of 2048 tokens x "
            "(32 Q + 8 K + 8 V heads), Q out [128, 32, 2048], K/V into their cache rows",
     "c2q": "C2 with Q in F16 as the pre-attention step writes it (no F32 Q read, no conversion)",
+    "nrx": "pre-attention step of C4 cross (mxfa_qk_norm_rope, no RoPE): QK-RMSNorm + F16 cast of B=2 x (3000 "
+           "tokens x 16 Q heads + 256 encoder tokens x 16 K + 16 V heads)",
+    "c4xq": "C4 cross with Q in F16 as the cross pre-attention step writes it",
 })
 BOUND = {"c1": "hbm", "c2": "mfma", "c3": "hbm", "c4s": "mfma", "c4x": "hbm", "c5": "hbm", "c4s8": "mfma", "c4x8": "hbm",
-         "c2m": "mfma", "c3m": "hbm", "c4xm": "hbm", "c2q": "mfma"}
+         "c2m": "mfma", "c3m": "hbm", "c4xm": "hbm", "c2q": "mfma", "c4xq": "hbm"}
 KERNEL = {"c1": "fa_decode", "c2": "fa_prefill", "c3": "fa_decode", "c4s": "fa_prefill", "c4x": "fa_prefill",
-          "c5": "fa_decode", "c4s8": "fa_prefill", "c4x8": "fa_prefill", "c2m": "fa_prefill", "c3m": "fa_decode", "c4xm": "fa_prefill", "c2q": "fa_prefill"}
+          "c5": "fa_decode", "c4s8": "fa_prefill", "c4x8": "fa_prefill", "c2m": "fa_prefill", "c3m": "fa_decode", "c4xm": "fa_prefill", "c2q": "fa_prefill",
+          "c4xq": "fa_prefill"}
 STRUCTURED = {"c2m": "c2", "c3m": "c3", "c4xm": "c4x"}   # structured-mask variant -> dense config
 
 
@@ -208,12 +212,16 @@ def time_set_rows(mx, torch, case, steps, warmup, rotate_bytes=ROTATE_BYTES):
 
 
 def time_norm_rope(mx, torch, steps, warmup, B=1, S=2048, Nh=32, Nkv=8, max_seq=2048,
-                   rotate_bytes=ROTATE_BYTES):
+                   rotate_bytes=ROTATE_BYTES, enc_S=None):
     """Fused pre-attention step timing on synthetic device data: (ms per call,
-    kernel avg ms, work, copies).  Copies rotate past the Infinity Cache."""
+    kernel avg ms, work, copies).  Copies rotate past the Infinity Cache.
+    enc_S given: the DiT cross-attention form (no RoPE; K/V of enc_S
+    encoder tokens into [128, enc_S, Nkv, B])."""
     from mxfa import cases as C
 
     D = 128
+    if enc_S is not None:
+        return _time_norm_cross(mx, torch, steps, warmup, B, S, Nh, Nkv, enc_S, rotate_bytes)
     H = Nh + 2 * Nkv
     w = C.norm_rope_work(B, S, Nh, Nkv)
     n_copies = int(min(32, max(1, math.ceil(rotate_bytes / w["bytes"]))))
@@ -245,6 +253,61 @@ def time_norm_rope(mx, torch, steps, warmup, B=1, S=2048, Nh=32, Nkv=8, max_seq=
     def step(i):
         q, k, v, qo, ko, vo = copies[i % n_copies]
         mx.qk_norm_rope(q, k, v, dqw, dkw, dpos, 1e-6, 1e6, qo, ko, vo, drows, stream=stream)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(steps):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    mx.timing_reset()
+    mx.timing_enable(True)
+    for i in range(steps):
+        step(i)
+    torch.cuda.synchronize()
+    mx.timing_enable(False)
+    tot, n = mx.timing_read("qk_norm_rope")
+    mx.timing_reset()
+    del copies
+    torch.cuda.empty_cache()
+    return ms, (tot / n if n else None), w, n_copies
+
+
+def _time_norm_cross(mx, torch, steps, warmup, B, S, Nh, Nkv, E, rotate_bytes):
+    from mxfa import cases as C
+
+    D = 128
+    w = C.norm_rope_work(B, S, Nh, Nkv, Skv=E)
+    n_copies = int(min(32, max(1, math.ceil(rotate_bytes / w["bytes"]))))
+    g = torch.Generator(device="cuda").manual_seed(1205)
+    qw = torch.ones(D, device="cuda") + 0.1 * torch.randn(D, device="cuda", generator=g)
+    kw = torch.ones(D, device="cuda") + 0.1 * torch.randn(D, device="cuda", generator=g)
+    wnb = (4, 4 * D, 4 * D, 4 * D)
+    dqw, dkw = mx.DeviceView(0, (D, 1, 1, 1), wnb, qw.data_ptr(), qw), mx.DeviceView(0, (D, 1, 1, 1), wnb, kw.data_ptr(), kw)
+    copies = []
+    for _ in range(n_copies):
+        xq = torch.randn(B, S, Nh, D, device="cuda", generator=g)
+        xkv = torch.randn(B, E, 2 * Nkv, D, device="cuda", generator=g)
+        qo = torch.empty(B, S, Nh, D, dtype=torch.float16, device="cuda")
+        ko = torch.empty(B, Nkv, E, D, dtype=torch.float16, device="cuda")
+        vo = torch.empty_like(ko)
+        kvnb = (4, 4 * D, 4 * D * 2 * Nkv, 4 * D * 2 * Nkv * E)
+        onb = (2, 2 * D, 2 * D * E, 2 * D * E * Nkv)
+        copies.append((mx.DeviceView(0, (D, Nh, S, B), (4, 4 * D, 4 * D * Nh, 4 * D * Nh * S), xq.data_ptr(), xq),
+                       mx.DeviceView(0, (D, Nkv, E, B), kvnb, xkv.data_ptr(), xkv),
+                       mx.DeviceView(0, (D, Nkv, E, B), kvnb, xkv.data_ptr() + 4 * D * Nkv, xkv),
+                       mx.DeviceView(1, (D, Nh, S, B), (2, 2 * D, 2 * D * Nh, 2 * D * Nh * S), qo.data_ptr(), qo),
+                       mx.DeviceView(1, (D, E, Nkv, B), onb, ko.data_ptr(), ko),
+                       mx.DeviceView(1, (D, E, Nkv, B), onb, vo.data_ptr(), vo)))
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step(i):
+        q, k, v, qo, ko, vo = copies[i % n_copies]
+        mx.qk_norm_rope(q, k, v, dqw, dkw, None, 1e-6, 1e6, qo, ko, vo, None, stream=stream)
 
     for i in range(warmup):
         step(i)
@@ -498,7 +561,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c4s8,c4x8,c2m,c3m,c4xm,c2q,kw2,kw3,kw5,nr2,dstep,dstepf")
+    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c4s8,c4x8,c2m,c3m,c4xm,c2q,c4xq,kw2,kw3,kw5,nr2,nrx,dstep,dstepf")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB copy (counter calibration under rocprofv3)")
@@ -532,14 +595,16 @@ def main():
             results[name] = summarize_set_rows(name, ms, kms, w, ncp)
             log(f"[bench] {name}: {json.dumps(results[name])}")
             continue
-        if name == "nr2":
-            ms, kms, w, ncp = time_norm_rope(mxfa, torch, args.steps, args.warmup)
+        if name in ("nr2", "nrx"):
+            kw_ = dict(B=2, S=3000, Nh=16, Nkv=16, enc_S=256) if name == "nrx" else {}
+            ms, kms, w, ncp = time_norm_rope(mxfa, torch, args.steps, args.warmup, **kw_)
             results[name] = summarize_set_rows(name, ms, kms, w, ncp)
             log(f"[bench] {name}: {json.dumps(results[name])}")
             continue
-        if name == "c2q":
-            case = C.with_q16(C.c2())
-            ms, kern, w, ncp = time_case(mxfa, torch, case, args.steps, args.warmup)
+        if name in ("c2q", "c4xq"):
+            case = C.with_q16(C.c2() if name == "c2q" else C.c4_cross())
+            rot = ROTATE_BYTES if BOUND[name] == "hbm" else None
+            ms, kern, w, ncp = time_case(mxfa, torch, case, args.steps, args.warmup, rot)
             results[name] = summarize(name, ms, kern, w, ncp)
             log(f"[bench] {name}: {json.dumps(results[name])}")
             continue

@@ -191,6 +191,12 @@ int mxfa_set_rows(mxfa_tensor *dst, const mxfa_tensor *src, const mxfa_tensor *r
  *               row s when rows is NULL (then M >= S)
  *   rows      : I64 | I32 [S, R] with B % R == 0, or NULL
  *
+ * positions == NULL selects DiT cross-attention's chain
+ * (src/dit-graph.h:317-346): QK-norm without RoPE (":333 no RoPE for
+ * cross-attention") and the K/V casts, with K/V of their own token count
+ * Skv (enc_S): k, v are [128, Nkv, Skv, B], k_out / v_out [128, M >= Skv,
+ * Nkv, B] (or rows [Skv, R]), while q / q_out keep S tokens.
+ *
  * Row ids outside [0, M) are skipped (ggml asserts).  Launches one kernel
  * on `hip_stream`, allocates nothing; MXFA_OK or a negative status. */
 typedef struct mxfa_norm_rope_params {

@@ -794,6 +794,23 @@ static void norm_rope_row(const float *x, const float *w, int pos, float eps, fl
     }
 }
 
+/* The same QK-RMSNorm without the rotation (DiT cross-attention,
+ * dit-graph.h:326-333): rms_norm(x, eps) * w for n rows of 128. */
+static void norm_row(const float *x, const float *w, float eps, float *y) {
+    double sum = 0.0;
+    for (int i = 0; i < 128; i++) sum += (double)(x[i] * x[i]);
+    const float mean = (float)(sum / 128);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int i = 0; i < 128; i++) {
+        const float t = x[i] * scale;
+        y[i] = t * w[i];
+    }
+}
+
+void ora_qk_norm(const float *x, const float *w, int64_t n_rows, float eps, float *y) {
+    for (int64_t r = 0; r < n_rows; r++) norm_row(x + r * 128, w, eps, y + r * 128);
+}
+
 void ora_qk_norm_rope(const float *q, const float *k, const float *v, const float *qw, const float *kw,
                       const int32_t *pos, int pos_per_batch, int Nh, int Nkv, int S, int B, float eps,
                       float freq_base, int clamp_v, float *q_o, float *k_o, float *v_o) {

@@ -13,6 +13,8 @@ fa_exact(q, k, v, mask, scale, ...) -> float64 [B, Sq, Nh, DV]
     fp64 two-pass softmax reference of the same op.
 qk_norm_rope(q, k, v, q_w, k_w, pos, eps, base, clamp_v) -> (q, k, v) F32
     restatement of ggml's CPU rms_norm * weight + NEOX rope (+ V clamp).
+qk_norm(x, w, eps) -> F32
+    the same rms_norm * weight without RoPE (DiT cross-attention).
 set_rows(dst, src, rows) -> skipped rows
     restatement of ggml's CPU set_rows (the KV-cache write), in place on dst.
 
@@ -94,6 +96,8 @@ def lib():
         L.ora_mad_f16.argtypes = [ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float]
         L.ora_qk_norm_rope.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_int] * 5 + [ctypes.c_float] * 2 + \
             [ctypes.c_int] + [ctypes.c_void_p] * 3
+        L.ora_qk_norm.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p]
+        L.ora_qk_norm.restype = None
         L.ora_set_rows.argtypes = [P, P, P]
         L.ora_set_rows.restype = ctypes.c_int64
         L.ora_set_force_scalar.argtypes = [ctypes.c_int]
@@ -212,6 +216,17 @@ def set_rows(dst: HostTensor, src: HostTensor, rows: HostTensor) -> int:
 
 
 # -- pre-attention work (rms_norm, NEOX rope) ----------------------------------
+
+def qk_norm(x, w, eps):
+    """x [..., 128] float32: rms_norm(x, eps) * w per row of 128, as ggml's
+    CPU ops compute it (the QK-norm of DiT cross-attention, no RoPE)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    assert x.shape[-1] == 128 and w.shape == (128,)
+    y = np.empty_like(x)
+    lib().ora_qk_norm(x.ctypes.data, w.ctypes.data, x.size // 128, eps, y.ctypes.data)
+    return y
+
 
 def qk_norm_rope(q, k, v, q_w, k_w, pos, eps, freq_base, clamp_v=False):
     """q [B, S, Nh, 128], k/v [B, S, Nkv, 128] float32, pos [S] or [B, S]

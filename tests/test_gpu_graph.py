@@ -199,7 +199,8 @@ def test_growth_under_capture_is_refused(mx):
     # freed, so the graph still replays correctly (interleaved with the
     # grown workspace's own calls).
     _, retired0 = mx.workspace_info()
-    big = C.lm_batch("t2", N=16, Nh=32, Nkv=8, max_seq=8192, lmin=7000, lmax=8192)
+    # 16 query rows per KV head need 4x the partials of the one-token batch
+    big = C.lm_single("t2", n_tokens=16, kv_pos=7000, Nh=32, Nkv=8, max_seq=8192)
     bq, bk, bv, bm = mx.upload(big.q), mx.upload(big.k), mx.upload(big.v), mx.upload(big.mask)
     Bb, Sqb, Nhb, DVb = big.out_shape
     bout = torch.zeros(Bb, Sqb, Nhb, DVb, device="cuda")

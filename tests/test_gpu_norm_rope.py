@@ -369,3 +369,78 @@ def test_pipeline_batched_decode(mx):
     L = Layer(mx, 22, B, 1, 32, 8, ms, 1, pos, pos.reshape(B, 1))
     # rows never written hold the sentinel: the lengths mask excludes them
     _pipeline(mx, L, 1536, dict(lengths=[int(p) + 1 for p in pos[:, 0]]), "batched decode")
+
+
+@pytest.mark.parametrize("out_type", [1, 30])
+def test_cross_attention_chain(mx, out_type):
+    """DiT cross-attention's pre-attention step (src/dit-graph.h:317-346):
+    QK-norm on S = 300 queries and on enc_S = 77 encoder keys, no RoPE
+    (positions = NULL), V cast; Q out [128, Nh, S, B], K/V [128, enc_S, Nkv,
+    B].  The kernel's rows against the oracle's (ora_qk_norm) cast to 16
+    bits, V bit-exact; then attention on its 16-bit Q with the encoder
+    padding mask against the oracle's F32 chain at the attention bar."""
+    import torch
+
+    import oracle
+    from mxfa import cases as C
+
+    B, S, E, Nh, Nkv = 2, 300, 77, 16, 8
+    rng = np.random.default_rng(4242 + out_type)
+    xq = (rng.standard_normal((B, S, Nh, D)) * 3).astype(np.float32)      # projection [D, Nh, S, B]
+    xkv = (rng.standard_normal((B, E, 2 * Nkv, D)) * 3).astype(np.float32)  # fused K|V [D, 2 Nkv, E, B]
+    qw = (1.0 + 0.3 * rng.standard_normal(D)).astype(np.float32)
+    kw = (1.0 + 0.3 * rng.standard_normal(D)).astype(np.float32)
+    dq, dkv = torch.from_numpy(xq).cuda(), torch.from_numpy(xkv).cuda()
+    dqw, dkw = torch.from_numpy(qw).cuda(), torch.from_numpy(kw).cuda()
+    qo = torch.zeros((B, S, Nh, D), dtype=torch.int16, device="cuda")
+    ko = torch.zeros((B, Nkv, E, D), dtype=torch.int16, device="cuda")
+    vo = torch.zeros_like(ko)
+    V = mx.DeviceView
+    qv = V(0, (D, Nh, S, B), (4, 4 * D, 4 * D * Nh, 4 * D * Nh * S), dq.data_ptr(), dq)
+    kvnb = (4, 4 * D, 4 * D * 2 * Nkv, 4 * D * 2 * Nkv * E)
+    kv_ = V(0, (D, Nkv, E, B), kvnb, dkv.data_ptr(), dkv)
+    vv_ = V(0, (D, Nkv, E, B), kvnb, dkv.data_ptr() + 4 * D * Nkv, dkv)
+    wnb = (4, 4 * D, 4 * D, 4 * D)
+    onb = (2, 2 * D, 2 * D * E, 2 * D * E * Nkv)
+    print(f"[cross] pre-attention S={S} enc_S={E} type={out_type}", flush=True)
+    mx.qk_norm_rope(qv, kv_, vv_, V(0, (D, 1, 1, 1), wnb, dqw.data_ptr(), dqw),
+                    V(0, (D, 1, 1, 1), wnb, dkw.data_ptr(), dkw), None, EPS, BASE,
+                    V(out_type, (D, Nh, S, B), (2, 2 * D, 2 * D * Nh, 2 * D * Nh * S), qo.data_ptr(), qo),
+                    V(out_type, (D, E, Nkv, B), onb, ko.data_ptr(), ko),
+                    V(out_type, (D, E, Nkv, B), onb, vo.data_ptr(), vo))
+    torch.cuda.synchronize()
+    rq = oracle.qk_norm(xq, qw, EPS)                                    # [B, S, Nh, D]
+    rk = oracle.qk_norm(xkv[:, :, :Nkv], kw, EPS).transpose(0, 2, 1, 3)  # [B, Nkv, E, D]
+    rv = xkv[:, :, Nkv:].transpose(0, 2, 1, 3)
+    for label, got, ref in (("q", qo, rq), ("k", ko, rk), ("v", vo, rv)):
+        g = got.cpu().numpy().view(np.uint16)
+        r16 = _to16(np.ascontiguousarray(ref), out_type)
+        if label == "v":
+            assert np.array_equal(g, r16), label
+            continue
+        diff = np.abs(_from16(g, out_type).astype(np.float64) - _from16(r16, out_type))
+        tol = _ulp16(_from16(r16, out_type), out_type)
+        assert np.all(diff <= tol), (label, float(diff.max()))
+        assert np.mean(g != r16) <= 0.01, (label, float(np.mean(g != r16)))
+
+    # attention over the step's outputs: Q is the permuted view [D, S, Nh, B]
+    pads = [0, 31]
+    live = np.arange(E)[None, :] < (E - np.asarray(pads))[:, None]                 # [B, E]
+    mbits = np.broadcast_to(np.where(live, 0, 0xFC00).astype(np.uint16)[:, None, :], (B, S, E)).copy()
+    dmask = torch.from_numpy(mbits.view(np.int16)).cuda()
+    q16 = V(out_type, (D, S, Nh, B), (2, 2 * D * Nh, 2 * D, 2 * D * Nh * S), qo.data_ptr(), qo)
+    kvnb16 = (2, 2 * D, 2 * D * E, 2 * D * E * Nkv)
+    out = mx.flash_attn_ext(q16, V(out_type, (D, E, Nkv, B), kvnb16, ko.data_ptr(), ko),
+                            V(out_type, (D, E, Nkv, B), kvnb16, vo.data_ptr(), vo),
+                            V(1, (E, S, 1, B), (2, 2 * E, 2 * E * S, 2 * E * S), dmask.data_ptr(), dmask),
+                            1.0 / D ** 0.5)
+    torch.cuda.synchronize()
+    got = mx.output_tensor(out).cpu().numpy()
+    qh = C.HostView(0, (D, S, Nh, B), (4, 4 * D * Nh, 4 * D, 4 * D * Nh * S), np.ascontiguousarray(rq).reshape(-1))
+    kh = C.HostView(out_type, (D, E, Nkv, B), kvnb16, ko.cpu().numpy().view(np.uint16).reshape(-1))
+    vh = C.HostView(out_type, (D, E, Nkv, B), kvnb16, vo.cpu().numpy().view(np.uint16).reshape(-1))
+    mh = C.HostView(1, (E, S, 1, B), (2, 2 * E, 2 * E * S, 2 * E * S), mbits.reshape(-1))
+    ref = oracle.fa_ggml(qh, kh, vh, mh, 1.0 / D ** 0.5, acc_f32=True)
+    m = row_metrics(got, ref)
+    print(f"[cross] chain type={out_type}: max_abs={m['max_abs']:.3e} min_cos={m['min_cos']:.7f}", flush=True)
+    assert m["max_abs"] <= MAX_ABS_TOL and m["min_cos"] >= ROW_COS_TOL, m

@@ -11,7 +11,9 @@ rows after rms_norm have unit RMS and the weight multiplies each dimension
 norm (a sign error in the rotation); a one-hot input rotates into dimension
 i + 64 with angle p * base^(-2i/128) (GPT-J pairing (2i, 2i+1) or a wrong
 frequency exponent); rotations compose by relative position (a transposed
-angle); V passes through untouched or clamped.
+angle); V passes through untouched or clamped.  The no-RoPE form (DiT
+cross-attention, ora_qk_norm) equals the rotating form at position 0 bit for
+bit (rope at position 0 multiplies by cos 0 = 1 and adds sin 0 = 0 terms).
 """
 from __future__ import annotations
 
@@ -161,3 +163,56 @@ def test_abi_argument_checks():
     bad_pos = mxfa.DeviceView(27, pos.ne, (8, 8 * S, 8 * S, 8 * S), pos.ptr).desc()
     assert mxfa.lib.mxfa_qk_norm_rope_supports(ref[0], ref[1], ref[2], ref[3], ref[4], ctypes.byref(bad_pos),
                                                ctypes.byref(prm), ref[6], ref[7], ref[8], None) == 0
+
+
+def test_norm_without_rope_is_position_zero():
+    """ora_qk_norm (the QK-norm of DiT cross-attention, no RoPE,
+    dit-graph.h:326-333) equals the rotating chain at position 0, bit for
+    bit, and normalises each row to unit RMS times the weight."""
+    o = _ora()
+    q, k = _rows((2, 3, 4, 128), 11) * 3, _rows((2, 3, 2, 128), 12)
+    w = np.linspace(0.25, 3.0, 128).astype(np.float32)
+    qo, ko, _ = o.qk_norm_rope(q, k, k, w, w, np.zeros(3, np.int32), EPS, BASE)
+    np.testing.assert_array_equal(o.qk_norm(q, w, EPS), qo)
+    np.testing.assert_array_equal(o.qk_norm(k, w, EPS), ko)
+    y = o.qk_norm(q, np.ones(128, np.float32), EPS)
+    np.testing.assert_allclose(np.sqrt((y.astype(np.float64) ** 2).mean(-1)), 1.0, atol=2e-6)
+    # scale invariance of rms_norm (eps negligible)
+    np.testing.assert_allclose(o.qk_norm(q * 8, w, 0.0), o.qk_norm(q, w, 0.0), rtol=1e-6, atol=1e-7)
+
+
+def test_abi_cross_attention_form():
+    """positions = NULL: no rotation, and K/V may hold enc_S tokens next to
+    Q's S (the DiT cross-attention chain, dit-graph.h:317-346); with
+    positions given the token counts must agree."""
+    import mxfa
+
+    D, Nh, Nkv, S, E = 128, 4, 2, 8, 5
+    q = _dev(0, (D, Nh, S, 1), (4, 4 * D, 4 * D * Nh, 4 * D * Nh * S), 0)
+    k = _dev(0, (D, Nkv, E, 1), (4, 4 * D, 4 * D * Nkv, 4 * D * Nkv * E), 0)
+    w = _dev(0, (D, 1, 1, 1), (4, 4 * D, 4 * D, 4 * D), 0)
+    pos = _dev(0, (S, 1, 1, 1), (4, 4 * S, 4 * S, 4 * S), 26)
+    qo = _dev(0, (D, Nh, S, 1), (2, 2 * D, 2 * D * Nh, 2 * D * Nh * S), 1)
+    ko = _dev(0, (D, E, Nkv, 1), (2, 2 * D, 2 * D * E, 2 * D * E * Nkv), 1)
+    P = ctypes.POINTER(mxfa.MxfaTensor)
+    prm = mxfa.MxfaNormRopeParams(EPS, BASE, 0)
+
+    def sup(pos_view, kk=k, kout=ko, rows=None):
+        d = [t.desc() for t in (q, kk, kk, w, w)]
+        dp = pos_view.desc() if pos_view is not None else None
+        o = [t.desc() for t in (qo, kout, kout)]
+        r = [ctypes.byref(x) for x in d]
+        ro = [ctypes.byref(x) for x in o]
+        return mxfa.lib.mxfa_qk_norm_rope_supports(r[0], r[1], r[2], r[3], r[4],
+                                                   ctypes.byref(dp) if dp is not None else None,
+                                                   ctypes.byref(prm), ro[0], ro[1], ro[2],
+                                                   ctypes.byref(rows.desc()) if rows is not None else None)
+
+    assert sup(None) == 1                 # no RoPE, 5 K/V tokens against 8 queries
+    assert sup(pos) == 0                  # RoPE needs one position per token of every row
+    short = _dev(0, (D, E - 1, Nkv, 1), ko.nb, 1)
+    assert sup(None, kout=short) == 0     # too few K/V rows
+    rows_e = _dev(0, (E, 1, 1, 1), (8, 8 * E, 8 * E, 8 * E), 27)
+    rows_s = _dev(0, (S, 1, 1, 1), (8, 8 * S, 8 * S, 8 * S), 27)
+    assert sup(None, rows=rows_e) == 1    # row ids count K/V tokens
+    assert sup(None, rows=rows_s) == 0
