@@ -581,9 +581,64 @@ void drain_pending() {
     g_pending.clear();
 }
 
+// -- the allocation-free variant's scratch ------------------------------------
+// A fixed device array per GPU (this code object's copy on each device)
+// stands in for the grow-only workspace: the tickets at its start, the split
+// partials or mask tile classes after them.  Host code never passes the
+// array's name to a kernel: it looks up each device's address once
+// (hipGetSymbolAddress) and uses that.
+constexpr size_t kScratchBytes = (size_t)8 << 20;      // 8 MiB per GPU, held until the process ends
+constexpr int64_t kScratchTickets = 65536;             // 256 KiB of split tickets
+constexpr size_t kScratchTicketBytes = (size_t)kScratchTickets * sizeof(int);
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+struct Scratch {
+    void *ws = nullptr;       // partials / classes
+    size_t ws_bytes = 0;
+    int *tickets = nullptr;
+    int64_t n_tickets = 0;
+};
+std::mutex g_scratch_mu;
+std::vector<void *> g_scratch_ptr;   // per device: the array's address, nullptr until set up
+
+// Set-up on the current device (first call there): the array's device
+// address, and one zero fill of its tickets (a kernel on `stream`; the
+// kernels leave every ticket at zero after that).  Refused while `stream`
+// is being captured.
+int scratch_of_device(hipStream_t stream, Scratch *out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(MXFA_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if ((size_t)dev >= g_scratch_ptr.size()) g_scratch_ptr.resize(dev + 1, nullptr);
+    if (!g_scratch_ptr[dev]) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return fail(MXFA_ERR_UNSUPPORTED,
+                        "the first mxfa_flash_attn_ext_noalloc call on a device sets up its scratch and must "
+                        "not be captured: call it once eagerly first");
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(MXFA_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        e = launch_fill_zero((int *)ptr, kScratchTickets, stream);
+        if (e != hipSuccess) return fail(MXFA_ERR_HIP, "scratch ticket fill: %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    uint8_t *base = (uint8_t *)g_scratch_ptr[dev];
+    out->tickets = (int *)base;
+    out->n_tickets = kScratchTickets;
+    out->ws = base + kScratchTicketBytes;
+    out->ws_bytes = kScratchBytes - kScratchTicketBytes;
+    return MXFA_OK;
+}
+
 // Plans and launches one validated call (dense `mask` or structured `sm`).
+// `fixed`: use that scratch instead of the stream's grow-only workspace
+// (the allocation-free entry point); a call that needs more fails.
 int run(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
-        const mxfa_params *params, mxfa_tensor *dst, void *hip_stream, const mxfa_mask_spec *sm) {
+        const mxfa_params *params, mxfa_tensor *dst, void *hip_stream, const mxfa_mask_spec *sm,
+        const Scratch *fixed = nullptr) {
     hipStream_t stream = (hipStream_t)hip_stream;
     Plan pl;
     make_plan(q, k, v, mask, params, dst, pl, sm);
@@ -591,8 +646,18 @@ int run(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const 
     if (!pl.prefill && (int64_t)pl.args.Nkv * pl.args.row_tiles > 65535)
         return fail(MXFA_ERR_UNSUPPORTED, "too many query rows per KV head for the decode kernel");
     int *tickets = nullptr;
-    int rc = ensure_workspace(pl.ws_bytes, pl.n_tickets, stream, &ws, &tickets);
-    if (rc != MXFA_OK) return rc;
+    if (fixed) {
+        if (pl.ws_bytes > fixed->ws_bytes || pl.n_tickets > fixed->n_tickets)
+            return fail(MXFA_ERR_UNSUPPORTED,
+                        "call needs %zu bytes of partials/classes and %lld tickets; the allocation-free scratch "
+                        "holds %zu bytes and %lld tickets",
+                        pl.ws_bytes, (long long)pl.n_tickets, fixed->ws_bytes, (long long)fixed->n_tickets);
+        ws = fixed->ws;
+        tickets = fixed->tickets;
+    } else {
+        const int rc = ensure_workspace(pl.ws_bytes, pl.n_tickets, stream, &ws, &tickets);
+        if (rc != MXFA_OK) return rc;
+    }
     FaArgs &a = pl.args;
     hipError_t e;
     if (pl.prefill) {
@@ -671,6 +736,18 @@ int mxfa_flash_attn_ext(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_t
     const int rc = check(q, k, v, mask, params, dst);
     if (rc != MXFA_OK) return rc;
     return run(q, k, v, mask, params, dst, hip_stream, nullptr);
+}
+
+int mxfa_flash_attn_ext_noalloc(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
+                                const mxfa_tensor *mask, const mxfa_params *params, mxfa_tensor *dst,
+                                void *hip_stream) {
+    if (!dst) return fail(MXFA_ERR_INVALID, "dst is required");
+    int rc = check(q, k, v, mask, params, dst);
+    if (rc != MXFA_OK) return rc;
+    Scratch sc;
+    rc = scratch_of_device((hipStream_t)hip_stream, &sc);
+    if (rc != MXFA_OK) return rc;
+    return run(q, k, v, mask, params, dst, hip_stream, nullptr, &sc);
 }
 
 int mxfa_reserve(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,

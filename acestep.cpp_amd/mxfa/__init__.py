@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "mxfa_flash_attn_ext",
     "mxfa_supports_masked",
     "mxfa_flash_attn_ext_masked",
+    "mxfa_flash_attn_ext_noalloc",
     "mxfa_reserve",
     "mxfa_qk_norm_rope",
     "mxfa_qk_norm_rope_supports",
@@ -131,6 +132,8 @@ def _load():
     L.mxfa_supports.restype = ctypes.c_int
     L.mxfa_flash_attn_ext.argtypes = [P, P, P, P, ctypes.POINTER(MxfaParams), P, ctypes.c_void_p]
     L.mxfa_flash_attn_ext.restype = ctypes.c_int
+    L.mxfa_flash_attn_ext_noalloc.argtypes = [P, P, P, P, ctypes.POINTER(MxfaParams), P, ctypes.c_void_p]
+    L.mxfa_flash_attn_ext_noalloc.restype = ctypes.c_int
     L.mxfa_qk_norm_rope.argtypes = [P, P, P, P, P, P, ctypes.POINTER(MxfaNormRopeParams), P, P, P, P,
                                     ctypes.c_void_p]
     L.mxfa_qk_norm_rope.restype = ctypes.c_int
@@ -243,6 +246,27 @@ def flash_attn_ext(q, k, v, mask, scale, max_bias=0.0, logit_softcap=0.0, prec=P
     p = make_params(scale, max_bias, logit_softcap, prec)
     rc = lib.mxfa_flash_attn_ext(refs[0], refs[1], refs[2], refs[3], ctypes.byref(p), refs[4],
                                  ctypes.c_void_p(int(stream)))
+    if rc != OK:
+        raise MxfaError(rc, last_error())
+    return dst
+
+
+def flash_attn_ext_noalloc(q, k, v, mask, scale, max_bias=0.0, logit_softcap=0.0, prec=PREC_F32,
+                           dst: Optional[DeviceView] = None, stream: Optional[int] = None) -> DeviceView:
+    """flash_attn_ext through mxfa_flash_attn_ext_noalloc: the same kernels
+    with the split partials, tickets and mask classes in the library's fixed
+    per-GPU scratch (no device allocation by the engine; `dst` is allocated
+    here with torch when None)."""
+    import torch
+
+    if dst is None:
+        dst = _out_view(q, v)
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    keep, refs = _descs(q, k, v, mask, dst)
+    p = make_params(scale, max_bias, logit_softcap, prec)
+    rc = lib.mxfa_flash_attn_ext_noalloc(refs[0], refs[1], refs[2], refs[3], ctypes.byref(p), refs[4],
+                                         ctypes.c_void_p(int(stream)))
     if rc != OK:
         raise MxfaError(rc, last_error())
     return dst

@@ -241,6 +241,25 @@ int mxfa_qk_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_ten
 int mxfa_reserve(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
                  const mxfa_params *params, void *hip_stream);
 
+/* Allocation-free variant of mxfa_flash_attn_ext (no counterpart in the
+ * reference or in ggml).  For callers that cannot allocate device memory:
+ * code under HIP graph capture, tight serving loops, hosts that forbid
+ * hipMalloc.  Same arguments, semantics and kernels as mxfa_flash_attn_ext,
+ * but the split-KV partials, split tickets and mask tile classes live in a
+ * fixed array of 8 MiB per GPU (65536 tickets plus 8 MiB - 256 KiB of
+ * partials/classes), held until the process ends; no hipMalloc, hipFree or
+ * allocating library call is made.  A call that needs more (decode with
+ * many query rows per KV head at long context; prefill masks with very
+ * many planes) fails with MXFA_ERR_UNSUPPORTED and launches nothing.  The
+ * first call on a device looks up the array and zero-fills its tickets
+ * (one kernel on `hip_stream`); it must not be captured.  Every call on a
+ * device shares that device's array, so calls that overlap in time on one
+ * GPU (on different streams, or a replayed graph next to an eager call)
+ * race; calls ordered on one stream do not. */
+int mxfa_flash_attn_ext_noalloc(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
+                                const mxfa_tensor *mask, const mxfa_params *params, mxfa_tensor *dst,
+                                void *hip_stream);
+
 /* Free the workspaces of every device and stream, retired buffers
  * included (synchronises each device first).  Graphs captured before the
  * call must not be replayed after it. */

@@ -1,0 +1,81 @@
+"""GPU: the allocation-free entry point (mxfa_flash_attn_ext_noalloc) against
+mxfa_flash_attn_ext through the C ABI.
+
+The two run the same kernels; the allocation-free one keeps the split-KV
+partials, split tickets and mask tile classes in the library's fixed
+per-GPU scratch array instead of the stream's grow-only workspace.  Each
+case makes two calls in a row, the second smaller than the first (the
+scratch keeps the first call's contents), and every output must equal the
+workspace entry point's bit for bit.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def mx():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import mxfa
+
+    return mxfa
+
+
+def _both(mx, case):
+    import torch
+
+    dq, dk, dv = mx.upload(case.q), mx.upload(case.k), mx.upload(case.v)
+    dm = mx.upload(case.mask) if case.mask is not None else None
+    ref = mx.flash_attn_ext(dq, dk, dv, dm, case.scale, case.max_bias, case.softcap)
+    torch.cuda.synchronize()
+    got = mx.flash_attn_ext_noalloc(dq, dk, dv, dm, case.scale, case.max_bias, case.softcap)
+    torch.cuda.synchronize()
+    return mx.output_tensor(got).cpu().numpy(), mx.output_tensor(ref).cpu().numpy()
+
+
+def test_noalloc_decode_matches_workspace_entry(mx):
+    """Split-KV decode (partials and tickets in the scratch): C3's batched
+    CFG decode, then a smaller batch with shorter sequences."""
+    from mxfa import cases as C
+
+    for label, case in (("C3", C.c3()),
+                        ("small", C.lm_batch("na", N=2, Nh=16, Nkv=8, max_seq=2048, lengths=[700, 1900]))):
+        print(f"[noalloc] decode {label}: q{tuple(case.q.ne)} k{tuple(case.k.ne)}", flush=True)
+        got, ref = _both(mx, case)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (label, float(np.abs(got - ref).max()))
+
+
+def test_noalloc_prefill_matches_workspace_entry(mx):
+    """Prefill with a dense mask (tile classes in the scratch): a causal
+    prompt of 1000 tokens, then a smaller one of 300 at an offset."""
+    from mxfa import cases as C
+
+    for label, case in (("c2-1000", C.c2(n_tokens=1000)),
+                        ("c1-300", C.lm_single("np", n_tokens=300, kv_pos=211, Nh=16, Nkv=8, max_seq=1024))):
+        print(f"[noalloc] prefill {label}: q{tuple(case.q.ne)} k{tuple(case.k.ne)}", flush=True)
+        got, ref = _both(mx, case)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (label, float(np.abs(got - ref).max()))
+
+
+def test_noalloc_allocates_nothing_in_the_engine(mx):
+    """The engine's own workspaces do not grow for allocation-free calls."""
+    import torch
+
+    from mxfa import cases as C
+
+    case = C.lm_batch("nz", N=4, Nh=32, Nkv=8, max_seq=4096, lmin=3000, lmax=4096)
+    dq, dk, dv, dm = mx.upload(case.q), mx.upload(case.k), mx.upload(case.v), mx.upload(case.mask)
+    out = mx.flash_attn_ext_noalloc(dq, dk, dv, dm, case.scale)
+    torch.cuda.synchronize()
+    live0, ret0 = mx.workspace_info()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        mx.flash_attn_ext_noalloc(dq, dk, dv, dm, case.scale, dst=out, stream=s.cuda_stream)
+    torch.cuda.synchronize()
+    assert mx.workspace_info() == (live0, ret0)
