@@ -56,6 +56,11 @@ constexpr int kStageBytes = 2 * kTileBytes;  // K + V
 constexpr int kPfLds = 2 * kStageBytes;      // double buffered: 64 KB
 constexpr uint32_t kXcds = 8;                // MI355X: workgroups go round-robin to 8 XCDs
 constexpr uint32_t kCusPerXcd = 32;          // 256 CUs
+#ifndef MXFA_PF_LOOK
+#define MXFA_PF_LOOK 2
+#endif
+constexpr int kPfLook = MXFA_PF_LOOK;        // LDS operand reads ahead of their MFMA (1..7)
+static_assert(kPfLook >= 1 && kPfLook <= 7, "operand ring holds 8");
 
 __global__ void __launch_bounds__(256) mask_classify_kernel(const FaArgs a, uint8_t *cls) {
     // One workgroup per (key tile, query tile, mask plane).  Each row of the
@@ -494,7 +499,9 @@ fa_prefill_kernel(const FaArgs a) {
     //   R4  PV a       | softmax of b
     //   R5  PV b
     // The code is laid out in issue order; sched_barrier fences keep it.
-    // Operand reads run two MFMAs ahead.
+    // The tile's 32 MFMA operands (K of half a and b, then V^T of half a and
+    // b) are read from LDS in one sequence kPfLook items ahead of the MFMA
+    // that consumes them (a ring of 8 operand registers).
     auto tile = [&](auto st_c, int kt) __attribute__((always_inline)) {
         const int cl = __builtin_amdgcn_readfirstlane(class_of(kt));
         const int key0 = kt * kPfBN;
@@ -503,15 +510,21 @@ fa_prefill_kernel(const FaArgs a) {
         const float g = general ? 1.0f : sl2;   // wave-uniform
         f32x16 sa, sb;
         u16x8 op[8];
+        // operand n of the tile: K(a) 0..7, K(b) 8..15, V^T(a) 16..23, V^T(b) 24..31
+        auto fetch = [&](int n) __attribute__((always_inline)) {
+            if (n < 8) op[n & 7] = kread(st_c, 0, n);
+            else if (n < 16) op[n & 7] = kread(st_c, 1, n - 8);
+            else if (n < 24) op[n & 7] = vread(st_c, 0, n - 16);
+            else if (n < 32) op[n & 7] = vread(st_c, 1, n - 24);
+        };
 
         // ---- R1: QK a ----
-        op[0] = kread(st_c, 0, 0);
-        op[1] = kread(st_c, 0, 1);
+#pragma unroll
+        for (int n = 0; n < kPfLook; n++) fetch(n);
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            if (t + 2 < 8) op[t + 2] = kread(st_c, 0, t + 2);
-            else op[t - 6] = kread(st_c, 1, t - 6);
-            sa = MF::run(__builtin_bit_cast(V8, op[t]), qb[t], t == 0 ? f32x16{} : sa);
+            fetch(t + kPfLook);
+            sa = MF::run(__builtin_bit_cast(V8, op[t & 7]), qb[t], t == 0 ? f32x16{} : sa);
             __builtin_amdgcn_sched_barrier(0);
         }
         if (general) general_x(sa, key0);
@@ -523,9 +536,8 @@ fa_prefill_kernel(const FaArgs a) {
         u16x8 pa[2], pb[2], pal[2], pbl[2];
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            if (t + 2 < 8) op[t + 2] = kread(st_c, 1, t + 2);
-            else op[t - 6] = vread(st_c, 0, t - 6);   // PV a operands 0, 1
-            sb = MF::run(__builtin_bit_cast(V8, op[t]), qb[t], t == 0 ? f32x16{} : sb);
+            fetch(8 + t + kPfLook);
+            sb = MF::run(__builtin_bit_cast(V8, op[(8 + t) & 7]), qb[t], t == 0 ? f32x16{} : sb);
             if (t == 0) mxa = half_max(sa);
             else pair(sa, t - 1, g, mneg0, pa, pal);
             if (t == 7) pair(sa, 7, g, mneg0, pa, pal);
@@ -560,11 +572,11 @@ fa_prefill_kernel(const FaArgs a) {
         // ---- R4: PV a | softmax b ----
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            if (i + 2 < 8) op[(i + 2) & 7] = vread(st_c, 0, i + 2);
-            else op[(i + 2) & 7] = vread(st_c, 1, i - 6);   // PV b operands 0, 1
-            o[i & 3] = MF::run(__builtin_bit_cast(V8, op[i & 7]), __builtin_bit_cast(V8, pa[i >> 2]), o[i & 3]);
+            fetch(16 + i + kPfLook);
+            o[i & 3] = MF::run(__builtin_bit_cast(V8, op[(16 + i) & 7]), __builtin_bit_cast(V8, pa[i >> 2]), o[i & 3]);
             if constexpr (kLo)
-                o[i & 3] = MF::run(__builtin_bit_cast(V8, op[i & 7]), __builtin_bit_cast(V8, pal[i >> 2]), o[i & 3]);
+                o[i & 3] = MF::run(__builtin_bit_cast(V8, op[(16 + i) & 7]), __builtin_bit_cast(V8, pal[i >> 2]),
+                                   o[i & 3]);
             pair(sb, i, g, mneg, pb, pbl);
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -574,10 +586,11 @@ fa_prefill_kernel(const FaArgs a) {
         // ---- R5: PV b ----
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            if (i + 2 < 8) op[(i + 2) & 7] = vread(st_c, 1, i + 2);
-            o[i & 3] = MF::run(__builtin_bit_cast(V8, op[i & 7]), __builtin_bit_cast(V8, pb[i >> 2]), o[i & 3]);
+            fetch(24 + i + kPfLook);
+            o[i & 3] = MF::run(__builtin_bit_cast(V8, op[(24 + i) & 7]), __builtin_bit_cast(V8, pb[i >> 2]), o[i & 3]);
             if constexpr (kLo)
-                o[i & 3] = MF::run(__builtin_bit_cast(V8, op[i & 7]), __builtin_bit_cast(V8, pbl[i >> 2]), o[i & 3]);
+                o[i & 3] = MF::run(__builtin_bit_cast(V8, op[(24 + i) & 7]), __builtin_bit_cast(V8, pbl[i >> 2]),
+                                   o[i & 3]);
             __builtin_amdgcn_sched_barrier(0);
         }
         lsum += la + lb;

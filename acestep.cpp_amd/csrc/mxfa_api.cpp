@@ -338,20 +338,23 @@ int check(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, cons
 // Validation of a structured mask (mxfa_mask_spec) for q's shape.
 int check_spec(const mxfa_mask_spec *sm, const mxfa_tensor *q) {
     if (!sm) return fail(MXFA_ERR_INVALID, "mask spec is required");
-    if (sm->flags & ~(MXFA_MASK_CAUSAL | MXFA_MASK_WINDOW | MXFA_MASK_LENGTHS))
+    if (sm->flags & ~(MXFA_MASK_CAUSAL | MXFA_MASK_WINDOW | MXFA_MASK_LENGTHS | MXFA_MASK_DEVICE))
         return fail(MXFA_ERR_INVALID, "unknown mask flags 0x%x", sm->flags);
+    const bool dev = (sm->flags & MXFA_MASK_DEVICE) != 0;
     const int64_t lim = (int64_t)1 << 30;
     const int64_t w = (sm->flags & MXFA_MASK_WINDOW) ? sm->window : 0;
-    if (w < 0) return fail(MXFA_ERR_INVALID, "window %d < 0", sm->window);
+    if (w < 0 || w >= lim) return fail(MXFA_ERR_INVALID, "window %d out of range", sm->window);
     if (sm->pos0 < 0 || sm->pos0 + q->ne[1] + w >= lim) return fail(MXFA_ERR_INVALID, "pos0 / window out of range");
+    if (dev && q->ne[1] + w >= lim) return fail(MXFA_ERR_INVALID, "Sq + window out of range");
     if (sm->flags & MXFA_MASK_LENGTHS) {
         if (!sm->lengths) return fail(MXFA_ERR_INVALID, "MXFA_MASK_LENGTHS without lengths");
         if (sm->n_lengths != 1 && sm->n_lengths != q->ne[3])
             return fail(MXFA_ERR_INVALID, "n_lengths %d must be 1 or B = %lld", sm->n_lengths, (long long)q->ne[3]);
         if (sm->n_lengths > kSmMaxLen)
             return fail(MXFA_ERR_UNSUPPORTED, "n_lengths %d > %d", sm->n_lengths, kSmMaxLen);
-        for (int i = 0; i < sm->n_lengths; i++)
-            if (sm->lengths[i] < 0) return fail(MXFA_ERR_INVALID, "lengths[%d] = %d < 0", i, sm->lengths[i]);
+        if (!dev)   // (device lengths are read, and clamped, by the kernels)
+            for (int i = 0; i < sm->n_lengths; i++)
+                if (sm->lengths[i] < 0) return fail(MXFA_ERR_INVALID, "lengths[%d] = %d < 0", i, sm->lengths[i]);
     }
     return MXFA_OK;
 }
@@ -359,15 +362,21 @@ int check_spec(const mxfa_mask_spec *sm, const mxfa_tensor *q) {
 void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
                const mxfa_params *p, mxfa_tensor *dst, Plan &pl, const mxfa_mask_spec *sm = nullptr) {
     FaArgs &a = pl.args;
-    if (sm && sm->flags) {
+    const bool sm_dev = sm && (sm->flags & MXFA_MASK_DEVICE);
+    if (sm && (sm->flags & ~MXFA_MASK_DEVICE)) {
         a.sm_flags = sm->flags;
         a.sm_window = (sm->flags & MXFA_MASK_WINDOW) ? sm->window : 0;
         a.sm_pos0 = (int32_t)sm->pos0;
         a.sm_nlen = 1;
+        if (sm_dev) a.sm_pos0_dev = sm->dev_pos0;
         if (sm->flags & MXFA_MASK_LENGTHS) {
             a.sm_nlen = sm->n_lengths;
-            for (int i = 0; i < sm->n_lengths; i++)
-                a.sm_len[i] = (int32_t)std::min<int64_t>(sm->lengths[i], k->ne[1]);
+            if (sm_dev) {
+                a.sm_len_dev = sm->lengths;
+            } else {
+                for (int i = 0; i < sm->n_lengths; i++)
+                    a.sm_len[i] = (int32_t)std::min<int64_t>(sm->lengths[i], k->ne[1]);
+            }
         }
     }
     a.q = (const char *)q->data;
@@ -447,7 +456,7 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     const int64_t max_splits = (a.Skv + kSplitKeyQuantum - 1) / kSplitKeyQuantum;
     int64_t n_splits = 1, chunk = 0;
     auto round_q = [](int64_t x) { return (x + kSplitKeyQuantum - 1) / kSplitKeyQuantum * kSplitKeyQuantum; };
-    if (a.sm_flags) {
+    if (a.sm_flags && !sm_dev) {
         // Structured mask: every (batch, kv head, row tile) stream covers
         // the keys its rows see; one chunk size for all of them, from the
         // total live work, so that every split carries the same work.

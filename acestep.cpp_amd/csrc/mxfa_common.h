@@ -37,7 +37,10 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 //   |pos0 + i - j| <= window      (kSmWindow: dit-sampler.h:282,
 //                                  cond-enc.h:317, :341)
 // -- the same as a dense F16 mask holding 0 there and -inf elsewhere.
-constexpr int kSmCausal = 1, kSmWindow = 2, kSmLengths = 4;
+// kSmDevice: lengths (and pos0 when sm_pos0_dev is set) live in device
+// memory and are read by the kernels when they run, so a captured launch
+// follows values the host rewrites between graph replays.
+constexpr int kSmCausal = 1, kSmWindow = 2, kSmLengths = 4, kSmDevice = 8;
 constexpr int kSmMaxLen = 64;   // per-batch lengths carried in the arguments
 
 // Arguments shared by the attention kernels (passed by value).
@@ -72,6 +75,8 @@ struct FaArgs {
     // structured mask (sm_flags == 0: none; then `mask` may hold a dense one)
     int32_t q16;                          // Q stored in K's 16-bit type (no conversion on load)
     int32_t sm_flags, sm_window, sm_pos0, sm_nlen;
+    const int32_t *sm_len_dev;            // kSmDevice: lengths in device memory (else sm_len)
+    const int32_t *sm_pos0_dev;           // kSmDevice: pos0 in device memory, or NULL (sm_pos0)
     int32_t sm_len[kSmMaxLen];
 };
 
@@ -107,12 +112,32 @@ __device__ __forceinline__ float max_half32(float x) {
 // Live keys [lo, hi) of query row iq1 of batch b under the structured mask
 // (both ends are non-decreasing in iq1, so the rows of a tile cover
 // [lo(first row), hi(last row)) and all of them see [lo(last), hi(first))).
+// With kSmDevice the values come from device memory (the host never calls
+// this for such a spec); they are clamped here, as the host checks the
+// others: pos0 to [0, 2^30), a negative length to 0.
+// The device values are read with relaxed agent-scope atomic loads: a plain
+// load would let the compiler fold "device pointer or kernel-argument array"
+// into one flat load through a selected pointer, which read wrong lengths.
+__device__ __forceinline__ int sm_dev_load(const int32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __host__ __device__ __forceinline__ void sm_row_range(const FaArgs &a, int b, int iq1, int &lo, int &hi) {
-    const int p = a.sm_pos0 + iq1;
+    int p0 = a.sm_pos0;
+#if defined(__HIP_DEVICE_COMPILE__)
+    if (a.sm_pos0_dev) {
+        const int d = sm_dev_load(a.sm_pos0_dev);
+        p0 = d < 0 ? 0 : (d > (1 << 30) ? (1 << 30) : d);
+    }
+#endif
+    const int p = p0 + iq1;
     lo = 0;
     hi = a.Skv;
     if (a.sm_flags & kSmLengths) {
-        const int len = a.sm_len[b % a.sm_nlen];
+        int len = a.sm_len[b % a.sm_nlen];
+#if defined(__HIP_DEVICE_COMPILE__)
+        if (a.sm_len_dev) len = sm_dev_load(a.sm_len_dev + b % a.sm_nlen);
+#endif
+        len = len < 0 ? 0 : len;
         hi = hi < len ? hi : len;
     }
     if (a.sm_flags & kSmCausal) hi = hi < p + 1 ? hi : p + 1;

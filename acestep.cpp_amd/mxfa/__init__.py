@@ -79,7 +79,7 @@ class MxfaNormRopeParams(ctypes.Structure):
     _fields_ = [("eps", ctypes.c_float), ("freq_base", ctypes.c_float), ("clamp_v", ctypes.c_int32)]
 
 
-MASK_CAUSAL, MASK_WINDOW, MASK_LENGTHS = 1, 2, 4
+MASK_CAUSAL, MASK_WINDOW, MASK_LENGTHS, MASK_DEVICE = 1, 2, 4, 8
 
 
 class MxfaMaskSpec(ctypes.Structure):
@@ -89,18 +89,34 @@ class MxfaMaskSpec(ctypes.Structure):
         ("pos0", ctypes.c_int64),
         ("n_lengths", ctypes.c_int32),
         ("lengths", ctypes.POINTER(ctypes.c_int32)),
+        ("dev_pos0", ctypes.c_void_p),
     ]
 
 
-def mask_spec(causal: bool = False, pos0: int = 0, window: Optional[int] = None, lengths=None):
+def mask_spec(causal: bool = False, pos0: int = 0, window: Optional[int] = None, lengths=None,
+              device_lengths=None, device_pos0=None):
     """A structured mask (mxfa_mask_spec).  Key j is live for query row i of
     batch b iff j < lengths[b % len(lengths)] (lengths given), j <= pos0 + i
-    (causal), |pos0 + i - j| <= window (window given)."""
+    (causal), |pos0 + i - j| <= window (window given).  device_lengths /
+    device_pos0: int32 torch tensors on the GPU read by the kernels at run
+    time (MXFA_MASK_DEVICE) instead of host values fixed at the call."""
     sp = MxfaMaskSpec()
+    dev = device_lengths is not None or device_pos0 is not None
     sp.flags = (MASK_CAUSAL if causal else 0) | (MASK_WINDOW if window is not None else 0) | \
-        (MASK_LENGTHS if lengths is not None else 0)
+        (MASK_LENGTHS if (lengths is not None or device_lengths is not None) else 0) | (MASK_DEVICE if dev else 0)
     sp.window = int(window or 0)
     sp.pos0 = int(pos0)
+    if dev:
+        keep = []
+        if device_lengths is not None:
+            sp.n_lengths = int(device_lengths.numel())
+            sp.lengths = ctypes.cast(ctypes.c_void_p(int(device_lengths.data_ptr())), ctypes.POINTER(ctypes.c_int32))
+            keep.append(device_lengths)
+        if device_pos0 is not None:
+            sp.dev_pos0 = int(device_pos0.data_ptr())
+            keep.append(device_pos0)
+        sp._keep = keep
+        return sp
     if lengths is not None:
         arr = (ctypes.c_int32 * len(lengths))(*[int(x) for x in lengths])
         sp.n_lengths = len(lengths)

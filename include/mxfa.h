@@ -121,17 +121,28 @@ int mxfa_flash_attn_ext(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_t
  * upload, no mask reads, no mask-classifier pass, and the split-KV decode
  * sizes its splits from the live lengths.  `lengths` is host memory read
  * during the call (n_lengths is 1 or B, at most 64; values >= 0); pos0 >= 0,
- * window >= 0, pos0 + Sq + window < 2^30. */
+ * window >= 0, pos0 + Sq + window < 2^30.
+ *
+ * MXFA_MASK_DEVICE: `lengths` (and `dev_pos0`, when not NULL, in place of
+ * pos0) point to device memory (int32) that the kernels read when they run,
+ * not at the call: a launch captured into a HIP graph then follows the
+ * values the host writes there between replays, as the reference's static
+ * decode graph does with its kv_len / position inputs (src/qwen3-lm.h:864-884).
+ * The decode split sizes then come from Skv, not from the live lengths.  The
+ * kernels clamp what they read: a negative length to 0, pos0 to [0, 2^30). */
 #define MXFA_MASK_CAUSAL  1
 #define MXFA_MASK_WINDOW  2
 #define MXFA_MASK_LENGTHS 4
+#define MXFA_MASK_DEVICE  8
 
 typedef struct mxfa_mask_spec {
     int32_t        flags;      /* MXFA_MASK_* bits */
     int32_t        window;     /* MXFA_MASK_WINDOW */
     int64_t        pos0;       /* absolute position of query row 0 (causal, window) */
     int32_t        n_lengths;  /* MXFA_MASK_LENGTHS: entries of lengths[] */
-    const int32_t *lengths;    /* MXFA_MASK_LENGTHS: live key count per batch */
+    const int32_t *lengths;    /* MXFA_MASK_LENGTHS: live key count per batch (device memory with
+                                  MXFA_MASK_DEVICE) */
+    const int32_t *dev_pos0;   /* MXFA_MASK_DEVICE: device int32 read for pos0, or NULL (use pos0) */
 } mxfa_mask_spec;
 
 int mxfa_supports_masked(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
@@ -233,10 +244,11 @@ int mxfa_qk_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_ten
  * graph keeps the workspace addresses of the stream it was captured on:
  * a later grow of that workspace retires the old buffers but keeps them
  * allocated until mxfa_release(), so the graph stays valid.  Replays must
- * not overlap in time with other mxfa calls on the capture stream.  A structured mask's host-side
- * values (pos0, window, lengths) are captured with the launch: for values
- * that change between replays use the dense mask, which lives in device
- * memory like the reference's.  (No counterpart in ggml: a backend calls
+ * not overlap in time with other mxfa calls on the capture stream.  A
+ * structured mask's host-side values (pos0, window, lengths) are captured
+ * with the launch: for lengths or positions that change between replays,
+ * set MXFA_MASK_DEVICE (they are then read from device memory at run time)
+ * or use the dense mask.  (No counterpart in ggml: a backend calls
  * mxfa_reserve from its graph set-up.) */
 int mxfa_reserve(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
                  const mxfa_params *params, void *hip_stream);

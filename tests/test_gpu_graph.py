@@ -325,3 +325,81 @@ def test_fused_decode_step_graph_replays_match_eager(mx):
         assert float(gs.out[0].abs().sum()) > 0
         # the token's cache row holds the step's K (not the warm-up's)
         assert not torch.equal(gs.cache_k[0][:, pos], torch.zeros_like(gs.cache_k[0][:, pos]))
+
+
+def test_device_lengths_follow_graph_replays(mx):
+    """Structured masks with device-resident lengths (MXFA_MASK_DEVICE): a
+    C3-shaped batched decode (8 sequences, 32/8 heads, cache 8192) captured
+    once and replayed for 4 tokens while the host rewrites the per-sequence
+    lengths (and the query) between replays, as the reference's static
+    decode graph does with its kv_len inputs (src/qwen3-lm.h:864-884).  Each
+    replay equals an eager call with the same device lengths bit for bit,
+    and the dense-mask call at the parity bar; no mask tensor exists."""
+    import torch
+
+    from conftest import MAX_ABS_TOL, ROW_COS_TOL, row_metrics
+    from mxfa import cases as C
+
+    c = C.c3()
+    N, Nh, Dh = 8, 32, 128
+    dk, dv = mx.upload(c.k), mx.upload(c.v)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    q = torch.zeros(N, Nh, 1, Dh, device="cuda")
+    qv = mx.DeviceView(0, (Dh, 1, Nh, N), (4, 4 * Dh, 4 * Dh, 4 * Dh * Nh), q.data_ptr(), q)
+    lens = torch.tensor(c.meta["lengths"], dtype=torch.int32, device="cuda")
+    spec = mx.mask_spec(device_lengths=lens)
+    out = torch.zeros(N, 1, Nh, Dh, device="cuda")
+    ov = mx.DeviceView(0, (Dh, Nh, 1, N), (4, 4 * Dh, 4 * Dh * Nh, 4 * Dh * Nh), out.data_ptr(), out)
+    ref = torch.zeros_like(out)
+    rv = mx.DeviceView(0, ov.ne, ov.nb, ref.data_ptr(), ref)
+    dense = torch.zeros_like(out)
+    dvw = mx.DeviceView(0, ov.ne, ov.nb, dense.data_ptr(), dense)
+    n_kv = int(c.k.ne[1])
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        mx.flash_attn_ext_masked(qv, dk, dv, spec, c.scale, dst=ov, stream=s.cuda_stream)   # sizes s's workspace
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with no_gc(), torch.cuda.stream(s):
+        with torch.cuda.graph(gr, stream=s):
+            mx.flash_attn_ext_masked(qv, dk, dv, spec, c.scale, dst=ov, stream=s.cuda_stream)
+    torch.cuda.synchronize()
+    base = [int(x) for x in c.meta["lengths"]]
+    for step in range(4):
+        new = [min(n_kv, L - 300 * step + 7 * step * (i % 3)) for i, L in enumerate(base)]
+        print(f"[graph device lengths] replay {step}: {new}", flush=True)
+        q.copy_(torch.randn(q.shape, generator=g))
+        lens.copy_(torch.tensor(new, dtype=torch.int32))
+        torch.cuda.synchronize()
+        out.zero_()
+        gr.replay()
+        torch.cuda.synchronize()
+        mx.flash_attn_ext_masked(qv, dk, dv, spec, c.scale, dst=rv)
+        j = torch.arange(n_kv, device="cuda")
+        mask = torch.where(j[None, :] < torch.tensor(new, device="cuda")[:, None], 0.0, float("-inf")).half()
+        mview = mx.DeviceView(1, (n_kv, 1, 1, N), (2, 2 * n_kv, 2 * n_kv, 2 * n_kv), mask.data_ptr(), mask)
+        mx.flash_attn_ext(qv, dk, dv, mview, c.scale, dst=dvw)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), step
+        m = row_metrics(out.cpu().numpy(), dense.cpu().numpy())
+        assert m["max_abs"] <= MAX_ABS_TOL and m["min_cos"] >= ROW_COS_TOL, (step, m)
+    del gr
+    torch.cuda.synchronize()
+    gc.collect()
+
+
+def test_device_pos0_prefill_equals_host_pos0(mx):
+    """A causal prompt continuation with pos0 in device memory equals the
+    same call with pos0 given on the host, bit for bit (prefill kernel)."""
+    import torch
+
+    from mxfa import cases as C
+
+    c = C.lm_single("dp", n_tokens=300, kv_pos=211, Nh=16, Nkv=8, max_seq=1024)
+    dq, dk, dv = mx.upload(c.q), mx.upload(c.k), mx.upload(c.v)
+    p0 = torch.tensor([211], dtype=torch.int32, device="cuda")
+    a = mx.flash_attn_ext_masked(dq, dk, dv, mx.mask_spec(causal=True, pos0=211), c.scale)
+    b = mx.flash_attn_ext_masked(dq, dk, dv, mx.mask_spec(causal=True, device_pos0=p0), c.scale)
+    torch.cuda.synchronize()
+    assert torch.equal(mx.output_tensor(a), mx.output_tensor(b))

@@ -9,6 +9,8 @@ check the C ABI's supports_op for the structured entry point (descriptor and
 spec checks only, no device)."""
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -107,8 +109,20 @@ def test_supports_masked():
     assert ok(mxfa.mask_spec())                                    # no mask
     assert ok(mxfa.mask_spec(window=128, lengths=[100]))
     bad = mxfa.mask_spec(causal=True)
-    bad.flags = 8
+    bad.flags = 16
     assert not ok(bad) and "flags" in mxfa.last_error()
+    # device-resident lengths / pos0 (MXFA_MASK_DEVICE): accepted without
+    # reading them on the host (placeholder device addresses)
+    dv = mxfa.mask_spec(causal=True)
+    dv.flags |= mxfa.MASK_DEVICE
+    dv.dev_pos0 = 1 << 20
+    assert ok(dv)
+    dl = mxfa.mask_spec(lengths=[7])
+    dl.flags |= mxfa.MASK_DEVICE
+    dl.lengths = ctypes.cast(ctypes.c_void_p(1 << 20), ctypes.POINTER(ctypes.c_int32))
+    assert ok(dl)
+    dl.lengths = None
+    assert not ok(dl)
     assert not ok(mxfa.mask_spec(window=-1))
     assert not ok(mxfa.mask_spec(causal=True, pos0=-5))
     assert not ok(mxfa.mask_spec(lengths=[1, 2, 3]))                # neither 1 nor B = 1
