@@ -329,6 +329,23 @@ def test_prefill_long_and_short_tiles(mx, mask):
     check(mx, c, f"long and short tiles ({mask})")
 
 
+@pytest.mark.parametrize("kind", ["random", "one_tile", "bf16_softcap_alibi", "gqa_broadcast"])
+def test_short_kv_many_query_tiles(mx, kind):
+    # the DiT cross-attention shape class: short K/V (1..4 tiles of 64 keys,
+    # the last one partial) under many query tiles and heads (more jobs than
+    # two rounds of workgroups), with masks, bf16, softcap + ALiBi and a
+    # K/V batch broadcast
+    if kind == "random":
+        c = _rand_case(300, B=3, Sq=700, Nh=32, Nkv=8, Skv=200, mask_heads=2)
+    elif kind == "one_tile":
+        c = _rand_case(301, B=2, Sq=1100, Nh=32, Nkv=4, Skv=64, mask=None)
+    elif kind == "bf16_softcap_alibi":
+        c = _rand_case(302, B=2, Sq=1030, Nh=32, Nkv=8, Skv=256, kv_type=30, softcap=30.0, max_bias=8.0)
+    else:
+        c = _rand_case(303, B=4, Bk=1, Sq=600, Nh=32, Nkv=2, Skv=129, mask=None)
+    check(mx, c, f"short K/V ({kind})")
+
+
 def test_workspace_grows_and_repeats(mx):
     from mxfa import cases
 
