@@ -78,6 +78,20 @@ struct Tile {
     int iq1, head;
 };
 
+// Splits of the (batch b, row tile rt) streams under a structured mask:
+// a.chunk keys each from the first key any row of the tile sees to the last
+// one (at least one split, which writes zeros when nothing is live).
+__device__ __forceinline__ void sm_tile_keys(const FaArgs &a, int b, int rt, int &lo, int &len) {
+    const int r0 = rt * 16, nr = min(16, a.M - r0);
+    int lo_f, hi_f, lo_l, hi_l;
+    sm_row_range(a, b, r0 / a.G, lo_f, hi_f);
+    sm_row_range(a, b, (r0 + nr - 1) / a.G, lo_l, hi_l);
+    lo = lo_f;
+    len = max(0, hi_l - lo_f);
+}
+__device__ __forceinline__ int sm_tile_splits(const FaArgs &a, int len) { return max(1, (len + a.chunk - 1) / a.chunk); }
+
+template <int MM>
 __device__ __forceinline__ Tile make_tile(const FaArgs &a) {
     Tile t;
     t.tid = threadIdx.x;
@@ -85,10 +99,30 @@ __device__ __forceinline__ Tile make_tile(const FaArgs &a) {
     t.wave = __builtin_amdgcn_readfirstlane(t.tid >> 6);   // wave-uniform
     t.c16 = t.lane & 15;
     t.g16 = t.lane >> 4;
-    t.split = blockIdx.x;
-    t.kvh = blockIdx.y / a.row_tiles;
-    t.rt = blockIdx.y % a.row_tiles;
-    t.b = blockIdx.z;
+    if (MM == kMaskStruct && a.dec_live > 0) {
+        // Live-split list (host lengths): workgroup i = j * Nkv + kv head,
+        // j running over the splits of (b, rt) in order, so that every
+        // workgroup streams live keys and none waits behind dead ones.
+        const int i = (int)blockIdx.x;
+        t.kvh = i % a.Nkv;
+        int j = i / a.Nkv, b = 0, rt = 0;
+        for (;;) {
+            int lo, len;
+            sm_tile_keys(a, b, rt, lo, len);
+            const int ns = sm_tile_splits(a, len);
+            if (j < ns || (b == a.B - 1 && rt == a.row_tiles - 1)) break;
+            j -= ns;
+            if (++rt == a.row_tiles) { rt = 0; b++; }
+        }
+        t.split = __builtin_amdgcn_readfirstlane(j);
+        t.rt = __builtin_amdgcn_readfirstlane(rt);
+        t.b = __builtin_amdgcn_readfirstlane(b);
+    } else {
+        t.split = blockIdx.x;
+        t.kvh = blockIdx.y / a.row_tiles;
+        t.rt = blockIdx.y % a.row_tiles;
+        t.b = blockIdx.z;
+    }
     t.bk = t.b / a.rk3;
     t.r = t.rt * 16 + t.c16;
     t.row_ok = t.r < a.M;
@@ -102,7 +136,9 @@ __device__ __forceinline__ Tile make_tile(const FaArgs &a) {
 // a.chunk keys from 0 (a.n_splits of them).  Structured masks: splits of
 // a.chunk keys from the first key any row of the tile sees, up to the last
 // one (the host sized a.chunk from the live lengths, so splits carry equal
-// work); workgroups past the stream's last split do nothing (skip).
+// work).  With host lengths the grid lists exactly those splits
+// (a.dec_live); with device lengths it is the dense grid and workgroups
+// past their stream's last split do nothing (skip).
 struct SplitRange {
     int k0, k1, ns;
     bool skip;
@@ -111,15 +147,12 @@ template <int MM>
 __device__ __forceinline__ SplitRange split_range(const FaArgs &a, const Tile &t) {
     SplitRange sr;
     if constexpr (MM == kMaskStruct) {
-        const int r0 = t.rt * 16, nr = min(16, a.M - r0);
-        int lo_f, hi_f, lo_l, hi_l;
-        sm_row_range(a, t.b, r0 / a.G, lo_f, hi_f);
-        sm_row_range(a, t.b, (r0 + nr - 1) / a.G, lo_l, hi_l);
-        const int len = max(0, hi_l - lo_f);
-        sr.ns = max(1, (len + a.chunk - 1) / a.chunk);
+        int lo, len;
+        sm_tile_keys(a, t.b, t.rt, lo, len);
+        sr.ns = sm_tile_splits(a, len);
         sr.skip = t.split >= sr.ns;
-        sr.k0 = len ? lo_f + t.split * a.chunk : 0;
-        sr.k1 = len ? min(hi_l, sr.k0 + a.chunk) : 0;
+        sr.k0 = len ? lo + t.split * a.chunk : 0;
+        sr.k1 = len ? min(lo + len, sr.k0 + a.chunk) : 0;
     } else {
         sr.ns = a.n_splits;
         sr.skip = false;
@@ -500,7 +533,7 @@ fa_decode_lds_kernel(const FaArgs a) {
     __shared__ int range_lds[2 * kDecWaves];
     __shared__ int last_lds;
 
-    const Tile t = make_tile(a);
+    const Tile t = make_tile<MM>(a);
     const SplitRange sr = split_range<MM>(a, t);
     if (sr.skip) return;   // past the stream's last split (uniform: no waits, no LDS, no ticket)
     const int lane = t.lane, c16 = t.c16, g16 = t.g16;
@@ -755,7 +788,7 @@ fa_decode_reg_kernel(const FaArgs a) {
     __shared__ int range_lds[2 * kDecWaves];
     __shared__ int last_lds;
 
-    const Tile t = make_tile(a);
+    const Tile t = make_tile<MM>(a);
     const SplitRange sr = split_range<MM>(a, t);
     if (sr.skip) return;   // past the stream's last split (uniform: no waits, no LDS, no ticket)
     const int c16 = t.c16, g16 = t.g16;
@@ -775,8 +808,7 @@ fa_decode_reg_kernel(const FaArgs a) {
     const float sc_in = a.softcap_in;
 
     const int k0 = sr.k0, k1 = sr.k1;
-    int lo = k0, hi = k1;
-    if constexpr (kDense) live_range(a, t, k0, k1, range_lds, lo, hi);
+    int lo = k0, hi = k1;   // live range (dense masks: scanned below)
     int rlo = 0, rhi = 0;
     if constexpr (MM == kMaskStruct) sm_row_range(a, t.b, t.iq1, rlo, rhi);
 
@@ -978,13 +1010,23 @@ fa_decode_reg_kernel(const FaArgs a) {
     // Blocks of this wave: kb0 + 128 n, n < n_blk.  Two register images
     // alternate; the loads of the next block are issued unconditionally
     // before the current block is computed, so the compiler's wait for the
-    // current image leaves them in flight.
+    // current image leaves them in flight.  Under a dense mask the first
+    // block from the split start goes out before the live-range scan (its
+    // loads and the scan's share one memory latency); it is the right block
+    // whenever the live range starts in the split's first 32 keys, as it
+    // does for every live split of a padding mask, and is loaded again
+    // otherwise.
     {
+        Blk x0, x1;
+        const int kb_spec = k0 + 32 * t.wave;
+        if constexpr (kDense) {
+            if (kb_spec < k1) load(kb_spec, x0);
+            live_range(a, t, k0, k1, range_lds, lo, hi);
+        }
         const int kb0 = k0 + ((lo - k0) & ~31) + 32 * t.wave;
         const int n_blk = (lo < hi && kb0 < hi) ? (hi - kb0 + 32 * kDecWaves - 1) / (32 * kDecWaves) : 0;
         if (n_blk > 0) {
-            Blk x0, x1;
-            load(kb0, x0);
+            if (!kDense || kb0 != kb_spec) load(kb0, x0);
             for (int n = 0;;) {
                 const int kb = kb0 + 32 * kDecWaves * n;
                 if (n + 1 == n_blk) {
@@ -1054,7 +1096,7 @@ static hipError_t launch_typed(const FaArgs &a, dim3 grid, hipStream_t stream) {
 }
 
 hipError_t launch_fa_decode(const FaArgs &a, int ktype, hipStream_t stream) {
-    const dim3 grid(a.n_splits, a.Nkv * a.row_tiles, a.B);
+    const dim3 grid = a.dec_live > 0 ? dim3((uint32_t)a.dec_live) : dim3(a.n_splits, a.Nkv * a.row_tiles, a.B);
     return timed_launch("fa_decode", stream, [&] {
         switch (ktype) {
             case T_F16: return launch_typed<T_F16>(a, grid, stream);

@@ -141,30 +141,6 @@ struct TileClasses {
     }
 };
 
-// Buffer resource over `bytes` bytes from `base`, offset addressed (stride
-// 0): a load at or past `bytes` returns zeros and touches no memory.
-__device__ __forceinline__ i32x4 buf_rsrc(const void *base, uint32_t bytes) {
-    const uint64_t b = (uint64_t)(uintptr_t)base;
-    i32x4 r;
-    r[0] = (int)__builtin_amdgcn_readfirstlane((uint32_t)b);
-    r[1] = (int)((uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) & 0xFFFFu);
-    r[2] = (int)__builtin_amdgcn_readfirstlane(bytes);
-    r[3] = 0x00020000;   // 32-bit data format, no swizzle, no stride
-    return r;
-}
-
-// HBM -> LDS copy of 16 bytes per lane through a buffer resource: lane l
-// reads base + voff(l) (zeros, and no memory access, when voff(l) + 16
-// exceeds the resource's size) and its bytes land at LDS address
-// lds_addr + 16*l.  Same wait contract as dma16 (callers wait with
-// MXFA_WAIT_VMCNT before reading the buffer).
-__device__ __forceinline__ void dma16_buf(const i32x4 &rsrc, uint32_t voff, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(lds_addr), "v"(voff), "s"(rsrc)
-                 : "memory", "m0");
-}
-
 // Max of a lane's value and the same register of lane l ^ 32 (one
 // v_permlane32_swap: lanes l and l ^ 32 hold the two key halves of a query).
 __device__ __forceinline__ float max_pair32(float x) {

@@ -64,6 +64,7 @@ constexpr int64_t kPrefillMinSq = 64;
 constexpr int64_t kSplitTargetWgs = 512;
 constexpr int kSplitKeyQuantum = 128;  // 4 waves x 32 keys
 constexpr int64_t kMaxDecodeSplits = 64;   // merge capacity of the decode kernel
+constexpr int kMaxLiveListTiles = 64;      // (batch, row tile) streams a live-split grid may list
 
 bool is_aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
@@ -475,7 +476,16 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
             }
         chunk = round_q(std::max<int64_t>({(total + kSplitTargetWgs - 1) / kSplitTargetWgs,
                                            (max_len + kMaxDecodeSplits - 1) / kMaxDecodeSplits, 1}));
-        for (int64_t len : lens) n_splits = std::max<int64_t>(n_splits, (len + chunk - 1) / chunk);
+        // the grid is the list of live splits, (b, rt, split) major, kv head
+        // minor, in the order the kernel walks them (each workgroup walks
+        // the (b, rt) list to find its split: short lists only)
+        int64_t live = 0;
+        for (int64_t len : lens) {
+            const int64_t ns = std::max<int64_t>(1, (len + chunk - 1) / chunk);
+            n_splits = std::max<int64_t>(n_splits, ns);
+            live += ns * a.Nkv;
+        }
+        if (lens.size() <= (size_t)kMaxLiveListTiles) a.dec_live = (int32_t)live;
     } else {
         if (base < kSplitTargetWgs)
             n_splits = std::min<int64_t>({max_splits, (kSplitTargetWgs + base - 1) / base, kMaxDecodeSplits});

@@ -66,6 +66,7 @@ struct FaArgs {
     uint32_t m_plane_bytes;               // prefill: bytes of one mask plane, (ne1 - 1) * nb1 + 2 * ne0
     // split-KV
     int32_t n_splits, chunk;
+    int32_t dec_live;                     // > 0: decode grid is the list of live splits (structured masks)
     float *part_o, *part_ml;
     int *tickets;                         // one per (b, kv head, row tile), zero between calls
     // prefill: per (mask plane, q tile, k tile) class (see fa_mfma.hip)
@@ -301,6 +302,30 @@ __device__ __forceinline__ void dma4(const void *g, void *lds_base) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
                  :
                  : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(g)
+                 : "memory", "m0");
+}
+
+// Buffer resource over `bytes` bytes from `base`, offset addressed (stride
+// 0): a load at or past `bytes` returns zeros and touches no memory.
+__device__ __forceinline__ i32x4 buf_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    i32x4 r;
+    r[0] = (int)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    r[1] = (int)((uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) & 0xFFFFu);
+    r[2] = (int)__builtin_amdgcn_readfirstlane(bytes);
+    r[3] = 0x00020000;   // 32-bit data format, no swizzle, no stride
+    return r;
+}
+
+// HBM -> LDS copy of 16 bytes per lane through a buffer resource: lane l
+// reads base + voff(l) (zeros, and no memory access, when voff(l) + 16
+// exceeds the resource's size) and its bytes land at LDS address
+// lds_addr + 16*l.  Same wait contract as dma16 (callers wait with
+// MXFA_WAIT_VMCNT before reading the buffer).
+__device__ __forceinline__ void dma16_buf(const i32x4 &rsrc, uint32_t voff, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_addr), "v"(voff), "s"(rsrc)
                  : "memory", "m0");
 }
 

@@ -285,6 +285,25 @@ def test_q8_0_shapes(mx, Sq, Skv, mask):
     check(mx, c, f"q8_0 Sq={Sq} Skv={Skv} mask={mask}")
 
 
+@pytest.mark.parametrize("Skv,lead", [(9, 0), (37, 4), (130, 8), (333, 12), (64, 4)])
+def test_q8_0_row_edges_and_alignment(mx, Skv, lead):
+    # Q8_0 rows read as 4-byte windows of 136-byte rows: key counts that end
+    # a 32-key block early (9, 37, 130, 333 keys) and views that start 4, 8
+    # or 12 bytes past a 16-byte boundary (the planes of 37 keys also
+    # alternate their alignment).  Every key is live (no mask): with 9 or
+    # 37 keys a wrong tail byte moves the output well past the bar.
+    from mxfa.cases import HostView
+
+    c = _rand_case(500 + Skv + lead, B=2, Sq=1, Nh=8, Nkv=2, Skv=Skv, kv_type=8, mask=None)
+    for name in ("k", "v"):
+        hv = getattr(c, name)
+        raw = np.ascontiguousarray(hv.buf).view(np.uint8).reshape(-1)
+        buf = np.zeros(raw.size + 16, dtype=np.uint8)
+        buf[lead:lead + raw.size] = raw
+        setattr(c, name, HostView(hv.type, hv.ne, hv.nb, buf, lead))
+    check(mx, c, f"q8_0 Skv={Skv} lead={lead}")
+
+
 def test_q8_0_broadcast_softcap_alibi(mx):
     c = _rand_case(95, B=4, Bk=1, Sq=2, Nh=8, Nkv=1, Skv=257, kv_type=8, mask_heads=8)
     check(mx, c, "q8_0 bk broadcast + per-head mask")
