@@ -27,7 +27,8 @@ kw2, kw3, and kw5 into a Q8_0 cache; GB/s of F32 read + converted row
 written + row ids, vs the HBM peak), the fused pre-attention step of C2
 (nr2: QK-RMSNorm + RoPE + F16 cast + cache write, GB/s vs the HBM peak) and
 C2's attention on the F16 Q that step writes (c2q).  Inputs of bandwidth-bound configs are rotated over enough device
-copies that consecutive steps do not hit in the 256 MB Infinity Cache.
+copies that consecutive steps do not hit in the 256 MB Infinity Cache.  "stream" is a calibration, not an
+engine op: a plain 1 GiB streaming read (libmxfa_calib.so), the HBM rate the decode figures compare with.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2,c3] [--no-cpu]
 """
@@ -81,6 +82,8 @@ DESCR.update({
     "nrx": "pre-attention step of C4 cross (mxfa_qk_norm_rope, no RoPE): QK-RMSNorm + F16 cast of B=2 x (3000 "
            "tokens x 16 Q heads + 256 encoder tokens x 16 K + 16 V heads)",
     "c4xq": "C4 cross with Q in F16 as the cross pre-attention step writes it",
+    "stream": "calibration, not an engine op: one streaming read of 1 GiB with 16-byte loads "
+              "(libmxfa_calib.so), the HBM rate a plain read reaches on this box",
 })
 BOUND = {"c1": "hbm", "c2": "mfma", "c3": "hbm", "c4s": "mfma", "c4x": "hbm", "c5": "hbm", "c4s8": "mfma", "c4x8": "hbm",
          "c2m": "mfma", "c3m": "hbm", "c4xm": "hbm", "c2q": "mfma", "c4xq": "hbm"}
@@ -542,6 +545,50 @@ def traffic_from_profiles():
     return None
 
 
+STREAM_BYTES = 1 << 30   # streaming-read calibration: 1 GiB, 4x the Infinity Cache
+
+
+def time_stream(torch, steps, warmup):
+    """The streaming-read calibration (config "stream"): one pass over
+    STREAM_BYTES of device memory with 16-byte loads, each workgroup over
+    one contiguous chunk, nothing written (libmxfa_calib.so, not the
+    engine), best of three grid sizes.  It is the anchor for the decode
+    kernels' HBM figures: what a plain read reaches on this box."""
+    import ctypes
+
+    lib = ctypes.CDLL(os.path.join(REPO, "acestep.cpp_amd", "lib", "libmxfa_calib.so"))
+    lib.mxfa_calib_stream_read.restype = ctypes.c_int
+    lib.mxfa_calib_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int,
+                                           ctypes.c_void_p]
+    buf = torch.ones(STREAM_BYTES // 4, dtype=torch.float32, device="cuda")
+    out = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    best = None
+    for blocks in (2048, 4096, 8192):
+        def launch():
+            rc = lib.mxfa_calib_stream_read(buf.data_ptr(), STREAM_BYTES, out.data_ptr(), blocks, stream)
+            if rc != 0:
+                raise RuntimeError(f"stream read launch failed ({rc})")
+        for _ in range(warmup):
+            launch()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            launch()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        if best is None or ms < best[0]:
+            best = (ms, blocks)
+    ms, blocks = best
+    gbs = STREAM_BYTES / (ms * 1e-3) / 1e9
+    del buf, out
+    torch.cuda.empty_cache()
+    return dict(workload=DESCR["stream"], ms=round(ms, 5), bytes=STREAM_BYTES, blocks=blocks, bound="hbm",
+                gbs=round(gbs, 2), frac_peak=round(gbs / PEAK_GBS, 4))
+
+
 def calibrate_copy(steps):
     """A plain device-to-device copy of COPY_BYTES, for scaling the
     FETCH_SIZE / WRITE_SIZE counters (run under rocprofv3 --pmc)."""
@@ -561,7 +608,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c4s8,c4x8,c2m,c3m,c4xm,c2q,c4xq,kw2,kw3,kw5,nr2,nrx,dstep,dstepf")
+    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c4s8,c4x8,c2m,c3m,c4xm,c2q,c4xq,kw2,kw3,kw5,nr2,nrx,dstep,dstepf,stream")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB copy (counter calibration under rocprofv3)")
@@ -606,6 +653,10 @@ def main():
             rot = ROTATE_BYTES if BOUND[name] == "hbm" else None
             ms, kern, w, ncp = time_case(mxfa, torch, case, args.steps, args.warmup, rot)
             results[name] = summarize(name, ms, kern, w, ncp)
+            log(f"[bench] {name}: {json.dumps(results[name])}")
+            continue
+        if name == "stream":
+            results[name] = time_stream(torch, max(20, args.steps // 4), 5)
             log(f"[bench] {name}: {json.dumps(results[name])}")
             continue
         if name in ("dstep", "dstepf"):

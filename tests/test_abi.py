@@ -30,6 +30,23 @@ def test_library_exports_every_declared_symbol():
     assert mxfa.status_string(-2) == "unsupported"
 
 
+def test_calibration_library_loads():
+    # bench.py's streaming-read calibration lives in its own library, beside
+    # the engine and outside its ABI
+    import ctypes
+
+    import torch  # noqa: F401  (one HIP runtime: torch's, loaded first)
+
+    lib = ctypes.CDLL(os.path.join(REPO, "acestep.cpp_amd", "lib", "libmxfa_calib.so"))
+    assert hasattr(lib, "mxfa_calib_stream_read")
+    # argument checks run before any device call
+    lib.mxfa_calib_stream_read.restype = ctypes.c_int
+    lib.mxfa_calib_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int,
+                                           ctypes.c_void_p]
+    assert lib.mxfa_calib_stream_read(None, 16, None, 1, None) != 0
+    assert lib.mxfa_calib_stream_read(1 << 20, 15, 1 << 21, 1, None) != 0
+
+
 def _dev(view, fake_ptr=1 << 20):
     import mxfa
 
