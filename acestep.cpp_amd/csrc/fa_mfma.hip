@@ -421,10 +421,15 @@ fa_prefill_kernel(const FaArgs a) {
             return;
         }
         const int kmax = a.Skv - key0 - 4 * h;   // keys 8j + i >= kmax lie past Skv
+        // (the four mask words go out together: one memory round trip)
+        u16x4 mw4[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            mw4[j] = __builtin_bit_cast(
+                u16x4, __builtin_amdgcn_raw_buffer_load_b64(mrs, mrow_off + 2u * (uint32_t)key0 + 16u * j, 0, 0));
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const u16x4 mw = __builtin_bit_cast(
-                u16x4, __builtin_amdgcn_raw_buffer_load_b64(mrs, mrow_off + 2u * (uint32_t)key0 + 16u * j, 0, 0));
+            const u16x4 mw = mw4[j];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int r = 4 * j + i;
