@@ -165,3 +165,18 @@ def test_softcap_alibi(mx):
     check(mx, c, dict(causal=True, pos0=170), "softcap + alibi prefill", bitwise=True)
     c = _rand_case(541, B=1, Sq=4, Nh=8, Nkv=2, Skv=300, mask=None, softcap=30.0, max_bias=8.0)
     check(mx, c, dict(causal=True, pos0=296), "softcap + alibi decode", bitwise=False)
+
+
+@pytest.mark.parametrize("B,Sq", [(3, 20), (22, 12)])
+def test_decode_split_grids(mx, B, Sq):
+    """Decode with host lengths, several row tiles per (batch, kv head):
+    3 batches x 5 row tiles use the grid that lists the live splits
+    ((batch, row tile, split) major, kv head minor); 22 batches x 3 row
+    tiles (66 streams, more than the list takes) use the dense grid whose
+    workgroups past their stream's last split return at once."""
+    rng = np.random.default_rng(600 + B)
+    c = _rand_case(600 + B + Sq, B=B, Sq=Sq, Nh=8, Nkv=2, Skv=900, mask=None)
+    lengths = [int(x) for x in rng.integers(0, 901, size=B)]
+    lengths[0] = 900
+    spec = dict(causal=True, pos0=900 - Sq, lengths=lengths)
+    check(mx, c, spec, f"decode grids B={B} Sq={Sq}", bitwise=False)
