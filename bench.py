@@ -615,7 +615,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this engine is measured on one GPU; --gpus {args.gpus} is not supported "
-              f"(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+              f"(this build measures one GPU; how the op would shard is a design note, not code)", file=sys.stderr)
         sys.exit(2)
 
     import torch
