@@ -154,38 +154,6 @@ __device__ __forceinline__ float sum_pair32(float x) {
     return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
-// acc *= alpha for a 16-register MFMA accumulator that stays in the
-// accumulation registers (AGPRs): read, multiply, write back in place.  The
-// O accumulators are only touched by the MFMAs and by this rare rescale, so
-// they never move between register files.
-__device__ __forceinline__ void scale_acc(f32x16 &o, float alpha) {
-    float t;
-    asm volatile(
-        "v_accvgpr_read_b32 %[t], %0\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %0, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %1\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %1, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %2\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %2, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %3\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %3, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %4\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %4, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %5\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %5, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %6\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %6, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %7\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %7, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %8\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %8, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %9\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %9, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %10\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %10, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %11\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %11, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %12\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %12, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %13\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %13, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %14\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %14, %[t]\n\t"
-        "v_accvgpr_read_b32 %[t], %15\n\tv_mul_f32 %[t], %[al], %[t]\n\tv_accvgpr_write_b32 %15, %[t]"
-        : "+a"(o[0]), "+a"(o[1]), "+a"(o[2]), "+a"(o[3]), "+a"(o[4]), "+a"(o[5]), "+a"(o[6]), "+a"(o[7]),
-          "+a"(o[8]), "+a"(o[9]), "+a"(o[10]), "+a"(o[11]), "+a"(o[12]), "+a"(o[13]), "+a"(o[14]), "+a"(o[15]),
-          [t] "=&v"(t)
-        : [al] "v"(alpha));
-}
-
-// sched_group_barrier classes
-enum : int { kSgMfma = 0x008, kSgValu = 0x402, kSgDsRead = 0x100 };
-
 // CAP: logit softcap on (a per-call constant; its tanh path is compiled only
 // into the instances that need it, so it costs the common path no registers).
 // SM: structured mask (a.sm_*): tile classes and per-element liveness are
