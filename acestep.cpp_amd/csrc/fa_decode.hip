@@ -117,6 +117,21 @@ __device__ __forceinline__ Tile make_tile(const FaArgs &a) {
         t.split = __builtin_amdgcn_readfirstlane(j);
         t.rt = __builtin_amdgcn_readfirstlane(rt);
         t.b = __builtin_amdgcn_readfirstlane(b);
+    } else if (a.dec_pair > 0) {
+        // Paired splits (two workgroups per CU): the grid's first half is
+        // dispatched one workgroup per CU and runs ahead of the second half
+        // (its waves are older), so every stream takes its even splits from
+        // the first half and its odd splits from the second, and the even
+        // split of each pair streams a.dec_pair keys, more than half.
+        const int L = (int)(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+        const int half = (int)(gridDim.x * gridDim.y * gridDim.z) / 2, hs = (int)gridDim.x / 2;
+        const bool first = L < half;
+        const int Lh = first ? L : L - half;
+        const int stream = Lh / hs;
+        t.split = __builtin_amdgcn_readfirstlane(2 * (Lh % hs) + (first ? 0 : 1));
+        t.kvh = __builtin_amdgcn_readfirstlane((stream % (int)gridDim.y) / a.row_tiles);
+        t.rt = __builtin_amdgcn_readfirstlane((stream % (int)gridDim.y) % a.row_tiles);
+        t.b = __builtin_amdgcn_readfirstlane(stream / (int)gridDim.y);
     } else {
         t.split = blockIdx.x;
         t.kvh = blockIdx.y / a.row_tiles;
@@ -153,6 +168,14 @@ __device__ __forceinline__ SplitRange split_range(const FaArgs &a, const Tile &t
         sr.skip = t.split >= sr.ns;
         sr.k0 = len ? lo + t.split * a.chunk : 0;
         sr.k1 = len ? min(lo + len, sr.k0 + a.chunk) : 0;
+    } else if (a.dec_pair > 0) {
+        // pair p = keys [2p chunk, (2p + 2) chunk): a.dec_pair for the even
+        // split, the rest for the odd one
+        sr.ns = a.n_splits;
+        sr.skip = false;
+        const int base = (t.split >> 1) * 2 * a.chunk;
+        sr.k0 = min(a.Skv, base + ((t.split & 1) ? a.dec_pair : 0));
+        sr.k1 = min(a.Skv, (t.split & 1) ? base + 2 * a.chunk : base + a.dec_pair);
     } else {
         sr.ns = a.n_splits;
         sr.skip = false;

@@ -65,6 +65,11 @@ constexpr int64_t kSplitTargetWgs = 512;
 constexpr int kSplitKeyQuantum = 128;  // 4 waves x 32 keys
 constexpr int64_t kMaxDecodeSplits = 64;   // merge capacity of the decode kernel
 constexpr int kMaxLiveListTiles = 64;      // (batch, row tile) streams a live-split grid may list
+constexpr int64_t kDecCus = 256;           // MI355X compute units
+#ifndef MXFA_DEC_PAIR_NUM
+#define MXFA_DEC_PAIR_NUM 10
+#endif
+constexpr int64_t kDecPairNum = MXFA_DEC_PAIR_NUM;   // even split's share of a pair, in eighths of a chunk x 2 / 2
 
 bool is_aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
@@ -494,6 +499,14 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     }
     a.n_splits = (int32_t)n_splits;
     a.chunk = (int32_t)chunk;
+    // Paired splits (fa_decode.hip, make_tile): a dense grid of exactly two
+    // workgroups per CU whose first half runs ahead of its second; the even
+    // split of each pair (first half) takes kDecPairNum/8 of the pair's
+    // 2 chunks / 2, rounded to the key quantum.
+    if (!a.sm_flags && kDecPairNum > 8 && n_splits % 2 == 0 && base * n_splits == 2 * kDecCus) {
+        const int64_t want = (chunk * kDecPairNum / 8 + kSplitKeyQuantum / 2) / kSplitKeyQuantum * kSplitKeyQuantum;
+        if (want > chunk && want < 2 * chunk) a.dec_pair = (int32_t)want;
+    }
     if (n_splits > 1) {
         const size_t rows = (size_t)a.B * a.Nkv * a.M * n_splits;
         pl.ws_bytes = rows * kD * sizeof(float) + rows * 2 * sizeof(float);

@@ -67,6 +67,7 @@ struct FaArgs {
     // split-KV
     int32_t n_splits, chunk;
     int32_t dec_live;                     // > 0: decode grid is the list of live splits (structured masks)
+    int32_t dec_pair;                     // > 0: paired splits, the even split of a pair streams dec_pair keys
     float *part_o, *part_ml;
     int *tickets;                         // one per (b, kv head, row tile), zero between calls
     // prefill: per (mask plane, q tile, k tile) class (see fa_mfma.hip)
