@@ -192,42 +192,47 @@ __device__ __forceinline__ const float *q_row(const FaArgs &a, const Tile &t) {
 // Q^T operand of the 16x16x32 MFMA: lane holds Q[row][32s + 8*g16 + e],
 // converted like ggml converts Q to K's vec-dot type (round to nearest even),
 // or loaded as it is when Q is already stored in that type (a.q16).
-template <int T>
-__device__ __forceinline__ void load_q16(const FaArgs &a, const Tile &t, typename Mfma16<T>::v8 (&qb)[4]) {
+// Q as Q8_0 (ggml quantize_row_q8_0: d = fp16(amax/127), q = rint(x*127/amax)
+// per 32-value block), laid out as the B operand of the i8 MFMA.
+// Q of the register kernel in two halves: q_issue loads the lane's raw Q
+// (F32, or 16-bit when a.q16), q_convert turns it into the MFMA operands
+// (the 16-bit type of the PV product, or Q8_0 as ggml quantises Q for a
+// Q8_0 K).  Between them the kernel issues its first K/V loads, so Q's
+// conversion waits for Q's own loads alone.
+struct QRaw {
+    f32x4 x[8];
+};
+__device__ __forceinline__ QRaw q_issue(const FaArgs &a, const Tile &t) {
+    QRaw r;
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.x[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (!t.row_ok) return r;
     if (a.q16) {
         const uint16_t *qh = (const uint16_t *)(a.q + (int64_t)t.iq1 * a.q_nb1 + (int64_t)t.head * a.q_nb2 +
                                                 (int64_t)t.b * a.q_nb3);
 #pragma unroll
+        for (int s = 0; s < 4; s++) r.x[2 * s] = __builtin_bit_cast(f32x4, *(const u16x8 *)(qh + 32 * s + 8 * t.g16));
+    } else {
+        const float *qp = q_row(a, t);
+#pragma unroll
         for (int s = 0; s < 4; s++) {
-            u16x8 x = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (t.row_ok) x = *(const u16x8 *)(qh + 32 * s + 8 * t.g16);
-            qb[s] = __builtin_bit_cast(typename Mfma16<T>::v8, x);
+            r.x[2 * s] = *(const f32x4 *)(qp + 32 * s + 8 * t.g16);
+            r.x[2 * s + 1] = *(const f32x4 *)(qp + 32 * s + 8 * t.g16 + 4);
         }
-        return;
     }
-    const float *qp = q_row(a, t);
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-        f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
-        if (t.row_ok) {
-            x0 = *(const f32x4 *)(qp + 32 * s + 8 * t.g16);
-            x1 = *(const f32x4 *)(qp + 32 * s + 8 * t.g16 + 4);
-        }
-        qb[s] = __builtin_bit_cast(typename Mfma16<T>::v8, cvt8<T>(x0, x1));
-    }
+    return r;
 }
-
-// Q as Q8_0 (ggml quantize_row_q8_0: d = fp16(amax/127), q = rint(x*127/amax)
-// per 32-value block), laid out as the B operand of the i8 MFMA.
-__device__ __forceinline__ void load_q8(const FaArgs &a, const Tile &t, long (&qq)[4], float (&dq)[4]) {
-    const float *qp = q_row(a, t);
+template <int T>
+__device__ __forceinline__ void q_convert16(const FaArgs &a, const QRaw &r, typename Mfma16<T>::v8 (&qb)[4]) {
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+        qb[s] = a.q16 ? __builtin_bit_cast(typename Mfma16<T>::v8, r.x[2 * s])
+                      : __builtin_bit_cast(typename Mfma16<T>::v8, cvt8<T>(r.x[2 * s], r.x[2 * s + 1]));
+}
+__device__ __forceinline__ void q_convert8(const QRaw &r, long (&qq)[4], float (&dq)[4]) {
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-        f32x4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = {0.f, 0.f, 0.f, 0.f};
-        if (t.row_ok) {
-            x0 = *(const f32x4 *)(qp + 32 * s + 8 * t.g16);
-            x1 = *(const f32x4 *)(qp + 32 * s + 8 * t.g16 + 4);
-        }
+        const f32x4 x0 = r.x[2 * s], x1 = r.x[2 * s + 1];
         float amax = 0.0f;
 #pragma unroll
         for (int e = 0; e < 4; e++) amax = fmaxf(amax, fmaxf(fabsf(x0[e]), fabsf(x1[e])));
@@ -252,32 +257,8 @@ __device__ __forceinline__ const uint16_t *mask_row(const FaArgs &a, int iq1, in
 
 // Live key range [lo, hi) of [k0, k1) over the mask rows of the tile's
 // rows (empty when nothing is live).  Called by the whole workgroup.
-__device__ void live_range(const FaArgs &a, const Tile &t, int k0, int k1, int *range_lds, int &lo, int &hi) {
-    const int r0 = t.rt * 16;
-    const int nr = min(16, a.M - r0);
-    // rows of one query share a mask row when the mask has one head plane
-    const int q_first = r0 / a.G, q_last = (r0 + nr - 1) / a.G;
-    const int n_scan = a.m_ne2 == 1 ? q_last - q_first + 1 : nr;
-    const int n8 = (k1 - k0 + 7) >> 3;
-    int first = INT32_MAX, last = -1;
-    for (int it = t.tid; it < n_scan * n8; it += 256) {
-        const int si = it / n8, k8 = k0 + 8 * (it - si * n8);
-        const int sq1 = a.m_ne2 == 1 ? q_first + si : (r0 + si) / a.G;
-        const int sh = a.m_ne2 == 1 ? 0 : t.kvh * a.G + (r0 + si) % a.G;
-        const uint16_t *row = mask_row(a, sq1, sh, t.b);
-        uint32_t livebits = 0;
-        if (a.mask_al16 && k8 + 8 <= k1) {
-            const u16x8 mv = *(const u16x8 *)(row + k8);
-#pragma unroll
-            for (int e = 0; e < 8; e++) livebits |= (mv[e] != 0xFC00u ? 1u : 0u) << e;
-        } else {
-            for (int e = 0; e < 8 && k8 + e < k1; e++) livebits |= (row[k8 + e] != 0xFC00u ? 1u : 0u) << e;
-        }
-        if (livebits) {
-            first = min(first, k8 + __builtin_ctz(livebits));
-            last = max(last, k8 + 31 - __builtin_clz(livebits));
-        }
-    }
+// Workgroup-wide [first, last] of the per-thread live ranges -> [lo, hi).
+__device__ void range_reduce(const Tile &t, int first, int last, int *range_lds, int &lo, int &hi) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
         first = min(first, __shfl_xor(first, off));
@@ -297,6 +278,89 @@ __device__ void live_range(const FaArgs &a, const Tile &t, int k0, int k1, int *
     }
     lo = first;
     hi = last + 1;
+}
+
+// Mask rows scanned for a tile: the tile's queries (one row each when the
+// mask has one head plane) or its rows.
+struct ScanRows {
+    int q_first, r0, n_scan;
+};
+__device__ __forceinline__ ScanRows scan_rows(const FaArgs &a, const Tile &t) {
+    ScanRows sr;
+    sr.r0 = t.rt * 16;
+    const int nr = min(16, a.M - sr.r0);
+    sr.q_first = sr.r0 / a.G;
+    const int q_last = (sr.r0 + nr - 1) / a.G;
+    sr.n_scan = a.m_ne2 == 1 ? q_last - sr.q_first + 1 : nr;
+    return sr;
+}
+__device__ __forceinline__ const uint16_t *scan_row(const FaArgs &a, const Tile &t, const ScanRows &sr, int si) {
+    const int sq1 = a.m_ne2 == 1 ? sr.q_first + si : (sr.r0 + si) / a.G;
+    const int sh = a.m_ne2 == 1 ? 0 : t.kvh * a.G + (sr.r0 + si) % a.G;
+    return mask_row(a, sq1, sh, t.b);
+}
+
+// Live range [lo, hi) of keys in [k0, k1) under a dense mask: keys whose
+// entry is -inf in every scanned row are dead.
+__device__ void live_range(const FaArgs &a, const Tile &t, int k0, int k1, int *range_lds, int &lo, int &hi) {
+    const ScanRows sr = scan_rows(a, t);
+    const int n8 = (k1 - k0 + 7) >> 3;
+    int first = INT32_MAX, last = -1;
+    for (int it = t.tid; it < sr.n_scan * n8; it += 256) {
+        const int si = it / n8, k8 = k0 + 8 * (it - si * n8);
+        const uint16_t *row = scan_row(a, t, sr, si);
+        uint32_t livebits = 0;
+        if (a.mask_al16 && k8 + 8 <= k1) {
+            const u16x8 mv = *(const u16x8 *)(row + k8);
+#pragma unroll
+            for (int e = 0; e < 8; e++) livebits |= (mv[e] != 0xFC00u ? 1u : 0u) << e;
+        } else {
+            for (int e = 0; e < 8 && k8 + e < k1; e++) livebits |= (row[k8 + e] != 0xFC00u ? 1u : 0u) << e;
+        }
+        if (livebits) {
+            first = min(first, k8 + __builtin_ctz(livebits));
+            last = max(last, k8 + 31 - __builtin_clz(livebits));
+        }
+    }
+    range_reduce(t, first, last, range_lds, lo, hi);
+}
+
+// The same scan in two halves, so that its loads go out ahead of a
+// kernel's first K/V loads and the reduction waits for them alone:
+// scan_issue loads each thread's 8-key group when one aligned 16-byte load
+// per thread covers the scan (16-byte aligned rows, k1 - k0 a multiple of
+// 8, at most 256 groups); otherwise scan_finish runs live_range.
+struct ScanPre {
+    u16x8 mv;
+    int k8;
+    bool one;
+};
+__device__ __forceinline__ ScanPre scan_issue(const FaArgs &a, const Tile &t, int k0, int k1) {
+    ScanPre p;
+    p.mv = u16x8{0xFC00u, 0xFC00u, 0xFC00u, 0xFC00u, 0xFC00u, 0xFC00u, 0xFC00u, 0xFC00u};
+    p.k8 = 0;
+    const ScanRows sr = scan_rows(a, t);
+    const int n8 = (k1 - k0) >> 3;
+    p.one = a.mask_al16 && ((k1 - k0) & 7) == 0 && sr.n_scan * n8 <= 256;   // uniform
+    if (p.one && t.tid < sr.n_scan * n8) {
+        const int si = t.tid / n8;
+        p.k8 = k0 + 8 * (t.tid - si * n8);
+        p.mv = *(const u16x8 *)(scan_row(a, t, sr, si) + p.k8);
+    }
+    return p;
+}
+__device__ __forceinline__ void scan_finish(const FaArgs &a, const Tile &t, const ScanPre &p, int k0, int k1,
+                                            int *range_lds, int &lo, int &hi) {
+    if (!p.one) {
+        live_range(a, t, k0, k1, range_lds, lo, hi);
+        return;
+    }
+    uint32_t livebits = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) livebits |= (p.mv[e] != 0xFC00u ? 1u : 0u) << e;
+    const int first = livebits ? p.k8 + __builtin_ctz(livebits) : INT32_MAX;
+    const int last = livebits ? p.k8 + 31 - __builtin_clz(livebits) : -1;
+    range_reduce(t, first, last, range_lds, lo, hi);
 }
 
 // 16 bytes stored at agent scope: global_store_dwordx4 with sc1, the
@@ -559,9 +623,12 @@ fa_decode_lds_kernel(const FaArgs a) {
     const Tile t = make_tile<MM>(a);
     const SplitRange sr = split_range<MM>(a, t);
     if (sr.skip) return;   // past the stream's last split (uniform: no waits, no LDS, no ticket)
+    // the live-range scan's loads go out first (dense mask), then Q's
+    ScanPre scan{};
+    if constexpr (MM == kMaskVec) scan = scan_issue(a, t, sr.k0, sr.k1);
+    const QRaw qraw = q_issue(a, t);
     const int lane = t.lane, c16 = t.c16, g16 = t.g16;
     V8 qb[4];
-    load_q16<KT>(a, t, qb);
     const float slope_l2 = alibi_slope(a, t.head) * kLog2e;
     const char *kbase = a.k + (int64_t)t.kvh * a.k_nb2 + (int64_t)t.bk * a.k_nb3;
     const char *vbase = a.v + (int64_t)t.kvh * a.v_nb2 + (int64_t)t.bk * a.v_nb3;
@@ -618,9 +685,11 @@ fa_decode_lds_kernel(const FaArgs a) {
     const int n_spec = min(MM == kMaskVec ? 1 : NST, nblk_spec);
     for (int s = 0; s < n_spec; s++) issue(kbw_spec + 64 * s, s);
 
+    q_convert16<KT>(a, qraw, qb);
     int lo = k0, hi = k1;
-    if constexpr (MM == kMaskVec) live_range(a, t, k0, k1, range_lds, lo, hi);
-    // the speculative stages have landed (they drain with the scan's loads)
+    if constexpr (MM == kMaskVec) scan_finish(a, t, scan, k0, k1, range_lds, lo, hi);
+    // the speculative stages have landed (they drain with Q's and the scan's
+    // loads: one memory latency for all three)
     MXFA_WAIT_VMCNT(0);
 
     const int base = lo < hi ? k0 + ((lo - k0) & ~63) : k0;
@@ -814,14 +883,16 @@ fa_decode_reg_kernel(const FaArgs a) {
     const Tile t = make_tile<MM>(a);
     const SplitRange sr = split_range<MM>(a, t);
     if (sr.skip) return;   // past the stream's last split (uniform: no waits, no LDS, no ticket)
+    constexpr bool kDense = MM == kMaskVec || MM == kMaskScalar;   // a dense mask is read
+    // the live-range scan's loads go out first (dense masks)
+    ScanPre scan{};
+    if constexpr (kDense) scan = scan_issue(a, t, sr.k0, sr.k1);
+    const QRaw qraw = q_issue(a, t);
     const int c16 = t.c16, g16 = t.g16;
     V8 qb[4];
     long qq[4];
     float dq[4];
-    if constexpr (kQ8) load_q8(a, t, qq, dq);
-    else load_q16<TV>(a, t, qb);
     const float slope_l2 = alibi_slope(a, t.head) * kLog2e;
-    constexpr bool kDense = MM == kMaskVec || MM == kMaskScalar;   // a dense mask is read
     const uint16_t *mrow = kDense ? mask_row(a, t.iq1, t.head, t.b) : nullptr;
     const int skv4 = (a.Skv + 3) & ~3;
     const char *kbase = a.k + (int64_t)t.kvh * a.k_nb2 + (int64_t)t.bk * a.k_nb3;
@@ -1033,19 +1104,22 @@ fa_decode_reg_kernel(const FaArgs a) {
     // Blocks of this wave: kb0 + 128 n, n < n_blk.  Two register images
     // alternate; the loads of the next block are issued unconditionally
     // before the current block is computed, so the compiler's wait for the
-    // current image leaves them in flight.  Under a dense mask the first
-    // block from the split start goes out before the live-range scan (its
-    // loads and the scan's share one memory latency); it is the right block
-    // whenever the live range starts in the split's first 32 keys, as it
-    // does for every live split of a padding mask, and is loaded again
-    // otherwise.
+    // current image leaves them in flight.  Under a dense mask the scan's
+    // loads go out first (at the kernel's start, then Q's), then the first
+    // block from the split start, and Q is converted and the scan reduced
+    // while that block is in flight; it is the right block whenever the live
+    // range starts in the split's first 32 keys, as it does for every live
+    // split of a padding mask, and is loaded again otherwise.  (A second
+    // speculative block measured slower: C5 28.2 against 27.0 us.)
     {
         Blk x0, x1;
         const int kb_spec = k0 + 32 * t.wave;
         if constexpr (kDense) {
             if (kb_spec < k1) load(kb_spec, x0);
-            live_range(a, t, k0, k1, range_lds, lo, hi);
         }
+        if constexpr (kQ8) q_convert8(qraw, qq, dq);
+        else q_convert16<TV>(a, qraw, qb);
+        if constexpr (kDense) scan_finish(a, t, scan, k0, k1, range_lds, lo, hi);
         const int kb0 = k0 + ((lo - k0) & ~31) + 32 * t.wave;
         const int n_blk = (lo < hi && kb0 < hi) ? (hi - kb0 + 32 * kDecWaves - 1) / (32 * kDecWaves) : 0;
         if (n_blk > 0) {
