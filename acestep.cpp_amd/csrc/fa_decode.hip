@@ -395,8 +395,21 @@ __device__ void merge_splits(const FaArgs &a, const Tile &t, int64_t pr0, int nr
     float *Linv = wl + 16 * kMaxSplits;      // [16]
     const int d = t.tid & (kD - 1);
     const int rA = t.tid >> 7, rB = rA + 2;
+    // The first 16 partials of rows rA and rB and the first 1024 (m, l)
+    // pairs go out together: one memory round trip.  (The workgroup's LDS
+    // is free here: its own merge data was read before the ticket's
+    // barriers, and a barrier would also wait for these loads.)
     float pa[16], pb[16];
+    float mv0[4], lv0[4];
     {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = t.tid + 256 * u;
+            const int r = i / ns, sp = i - r * ns;
+            const float *pm = a.part_ml + ((pr0 + r) * stride + sp) * 2;
+            mv0[u] = i < nr * ns ? ld_dev(pm) : 0.0f;
+            lv0[u] = i < nr * ns ? ld_dev(pm + 1) : 0.0f;
+        }
         const float *poA = a.part_o + (pr0 + rA) * stride * kD + d;
         const float *poB = a.part_o + (pr0 + rB) * stride * kD + d;
 #pragma unroll
@@ -405,7 +418,6 @@ __device__ void merge_splits(const FaArgs &a, const Tile &t, int64_t pr0, int nr
             pb[u] = (rB < nr && u < ns) ? ld_dev(poB + (int64_t)u * kD) : 0.0f;
         }
     }
-    __syncthreads();                         // lds is free (waves' merge data consumed)
     for (int i0 = 0; i0 < nr * ns; i0 += 256 * 4) {
         float mv[4], lv[4];
 #pragma unroll
@@ -413,8 +425,8 @@ __device__ void merge_splits(const FaArgs &a, const Tile &t, int64_t pr0, int nr
             const int i = i0 + t.tid + 256 * u;
             const int r = i / ns, sp = i - r * ns;
             const float *pm = a.part_ml + ((pr0 + r) * stride + sp) * 2;
-            mv[u] = i < nr * ns ? ld_dev(pm) : 0.0f;
-            lv[u] = i < nr * ns ? ld_dev(pm + 1) : 0.0f;
+            mv[u] = i0 == 0 ? mv0[u] : (i < nr * ns ? ld_dev(pm) : 0.0f);
+            lv[u] = i0 == 0 ? lv0[u] : (i < nr * ns ? ld_dev(pm + 1) : 0.0f);
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -446,13 +458,17 @@ __device__ void merge_splits(const FaArgs &a, const Tile &t, int64_t pr0, int nr
         const float *po = a.part_o + (pr0 + r) * stride * kD + d;
         float acc = 0.0f;
         for (int s0 = 0; s0 < ns; s0 += 16) {
-            float ov[16];
+            // (the 16 weights are read together, past ns too: a row holds
+            // kMaxSplits of them, and those past ns are not used)
+            float ov[16], wv[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) wv[u] = wm[r * kMaxSplits + s0 + u];
 #pragma unroll
             for (int u = 0; u < 16; u++)
                 ov[u] = (s0 == 0 && have_pre) ? pre[u] : (s0 + u < ns ? ld_dev(po + (int64_t)(s0 + u) * kD) : 0.0f);
 #pragma unroll
             for (int u = 0; u < 16; u++)
-                if (s0 + u < ns) acc = fmaf(wm[r * kMaxSplits + s0 + u], ov[u], acc);
+                if (s0 + u < ns) acc = fmaf(wv[u], ov[u], acc);
         }
         const int rg = t.rt * 16 + r;
         const int iq1o = rg / a.G, heado = t.kvh * a.G + rg % a.G;
