@@ -195,9 +195,9 @@ fa_prefill_kernel(const FaArgs a) {
         qt = __builtin_amdgcn_readfirstlane(a.n_qt - 1 - (int)(r / (uint32_t)a.G));
         b = __builtin_amdgcn_readfirstlane((int)(u / (uint32_t)a.Nkv));
         head = __builtin_amdgcn_readfirstlane((int)(u % (uint32_t)a.Nkv) * a.G + (int)(r % (uint32_t)a.G));
-        second = rnd == 1;
+        second = rnd == 1 && n_x >= 2 * kCusPerXcd;   // (every CU of the XCD holds a pair)
     }
-    // The two workgroups of the first pair start together, and both would
+    // The two workgroups of a CU's first pair start together, and both would
     // first fetch Q (64 KB in F32) and their first tile.  The second one
     // waits ~2 us (s_sleep 64: 64 x 64 clocks) so that the first pair's
     // fetches do not share one burst: the first workgroup (the long causal
