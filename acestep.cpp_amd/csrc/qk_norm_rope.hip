@@ -39,13 +39,38 @@ __device__ __forceinline__ uint16_t to16(float x) {
 // Rows of one token: [0, Nh) Q heads, [Nh, Nh + Nkv) K heads, then V heads.
 constexpr int kGroups = 3;   // 16-row groups a workgroup loads before it computes (48-row tokens: one pass)
 
+// One 32-bit half of a double moved across lanes by a DPP pattern.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, (uint64_t)lo | ((uint64_t)hi << 32));
+}
+
+// Sum over the 16 lanes of a row, left in every lane of it: partners 1 and 2
+// apart (quad permutations), then the mirrored quads and the mirrored
+// halves. Each step adds a value and its partner's, and the partner adds the
+// same two (addition commutes), so all 16 lanes hold the same bits.
+__device__ __forceinline__ double row16_sum(double v) {
+    v += dpp_f64<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+    v += dpp_f64<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+    v += dpp_f64<0x141>(v);   // row_half_mirror: quad 0 <-> 1, 2 <-> 3
+    v += dpp_f64<0x140>(v);   // row_mirror: half 0 <-> 1
+    return v;
+}
+
 // One workgroup per token (s, b), 4 waves.  A row belongs to 16 lanes: lane
 // j of the 16 holds dims 4j..4j+3 and 64+4j..64+4j+3 (the pairs it rotates,
-// two 16-byte loads), so a wave covers 4 rows per step and the row's sum of
-// squares takes 4 cross-lane steps.  Row h = 16 g + 4 wave + lane / 16 for
-// group g.  The pair angles depend on the token's position only: lane l
-// forms pair l's chain of multiplications and its sin/cos once per token,
-// while the row loads are in flight, and the row lanes fetch theirs.
+// two 16-byte loads), so a wave covers 4 rows per step.  Row h = 16 g +
+// 4 wave + lane / 16 for group g.  Each wave issues all its row loads
+// first, non-temporal (the F32 rows are read once; the 16-bit outputs are
+// stored normally, attention reads them next).  While they are in flight,
+// wave 0 forms the 64 pair angles of the token's position (one chain of
+// multiplications and one sincosf per lane) and wave 1 stages the two norm
+// weight rows; both go through LDS to the other waves, behind one barrier.
+// A group in which the wave has no row of the token (K/V past the encoder's
+// tokens in the cross form) is skipped after its loads.
 template <int OT>
 __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const NormRopeArgs a) {
     // (no contraction into fma: each product and sum rounds as written)
@@ -58,6 +83,13 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const NormRopeArgs a)
     const int H = a.Nh + 2 * a.Nkv;
     const bool q_on = s < a.S, kv_on = s < a.Skv;
 
+    __shared__ float sin_lds[64], cos_lds[64];   // pair angles' sine and cosine
+    __shared__ f32x4 w_lds[64];                  // q_w (32 x 4 floats), then k_w
+
+    // weight rows first, so that the wait for them leaves the row loads in flight
+    f32x4 wreg = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (wave == 1) wreg = *(const f32x4 *)((lane < 32 ? a.q_w : a.k_w) + 4 * (lane & 31));
+
     // K/V destination row of this token (uniform); out of range: skipped
     int64_t r = s;
     if (a.rows && kv_on) {
@@ -67,49 +99,56 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const NormRopeArgs a)
     const bool kv_ok = kv_on && r >= 0 && r < a.kv_rows;
     const int pos = a.rope ? a.pos[s + (int64_t)(a.pos_per_batch ? b : 0) * a.S] : 0;
 
+    f32x4 sn4 = f32x4{0.f, 0.f, 0.f, 0.f}, cs4 = f32x4{1.f, 1.f, 1.f, 1.f};
     for (int g0 = 0; g0 < H; g0 += 16 * kGroups) {
         f32x4 lo[kGroups], hi[kGroups];
         int kind[kGroups], hh[kGroups];
 #pragma unroll
         for (int g = 0; g < kGroups; g++) {
             const int h = g0 + 16 * g + 4 * wave + sub;
-            lo[g] = hi[g] = f32x4{0.f, 0.f, 0.f, 0.f};
             kind[g] = h < a.Nh ? (q_on ? 0 : 3) : (h < H ? (kv_on ? (h < a.Nh + a.Nkv ? 1 : 2) : 3) : 3);
             hh[g] = kind[g] == 0 ? h : (kind[g] == 1 ? h - a.Nh : h - a.Nh - a.Nkv);
-            if (kind[g] < 3) {
-                const char *src = kind[g] == 0 ? a.q : (kind[g] == 1 ? a.k : a.v);
-                const int64_t *nb = kind[g] == 0 ? a.q_nb : (kind[g] == 1 ? a.k_nb : a.v_nb);
-                const float *x = (const float *)(src + (int64_t)hh[g] * nb[0] + (int64_t)s * nb[1] +
-                                                 (int64_t)b * nb[2]);
-                lo[g] = *(const f32x4 *)(x + 4 * j);
-                hi[g] = *(const f32x4 *)(x + 64 + 4 * j);
-            }
+            // Base and strides are selected as values (a pointer into the
+            // argument block would be read through memory, with a wait), and
+            // a row that does not exist reads the weight row instead of
+            // branching round its load (the branch's join would wait for the
+            // data): the loads of all groups issue back to back.
+            const int kd = kind[g];
+            const char *src = kd == 0 ? a.q : (kd == 1 ? a.k : a.v);
+            const int64_t nb0 = kd == 0 ? a.q_nb[0] : (kd == 1 ? a.k_nb[0] : a.v_nb[0]);
+            const int64_t nb1 = kd == 0 ? a.q_nb[1] : (kd == 1 ? a.k_nb[1] : a.v_nb[1]);
+            const int64_t nb2 = kd == 0 ? a.q_nb[2] : (kd == 1 ? a.k_nb[2] : a.v_nb[2]);
+            const float *x = kd < 3 ? (const float *)(src + (int64_t)hh[g] * nb0 + (int64_t)s * nb1 + (int64_t)b * nb2)
+                                    : a.q_w;
+            lo[g] = __builtin_nontemporal_load((const f32x4 *)(x + 4 * j));
+            hi[g] = __builtin_nontemporal_load((const f32x4 *)(x + 64 + 4 * j));
         }
-        const f32x4 qw0 = *(const f32x4 *)(a.q_w + 4 * j), qw1 = *(const f32x4 *)(a.q_w + 64 + 4 * j);
-        const f32x4 kw0 = *(const f32x4 *)(a.k_w + 4 * j), kw1 = *(const f32x4 *)(a.k_w + 64 + 4 * j);
-        // angle of pair `lane`: `lane` float multiplications from theta_0 =
-        // pos; one sincosf per lane, then lane j of each 16 fetches the
-        // values of pairs 4j..4j+3 from lanes 4j..4j+3
-        float sn[4] = {0.f, 0.f, 0.f, 0.f}, cs[4] = {1.f, 1.f, 1.f, 1.f};
-        if (a.rope) {
-            float th = 0.f, t = (float)pos;
+        if (g0 == 0) {
+            if (wave == 1) w_lds[lane] = wreg;
+            if (wave == 0 && a.rope) {
+                // angle of pair `lane`: `lane` float multiplications from
+                // theta_0 = pos, then one sincosf
+                float th = 0.f, t = (float)pos;
 #pragma unroll
-            for (int i = 0; i < 64; i++) {
-                th = i == lane ? t : th;
-                t *= a.theta_scale;
+                for (int i = 0; i < 64; i++) {
+                    th = i == lane ? t : th;
+                    t *= a.theta_scale;
+                }
+                float sn1, cs1;
+                sincosf(th, &sn1, &cs1);
+                sin_lds[lane] = sn1;
+                cos_lds[lane] = cs1;
             }
-            float sn1, cs1;
-            sincosf(th, &sn1, &cs1);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int src = 4 * (4 * j + e);   // byte address of lane 4j + e
-                sn[e] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, sn1)));
-                cs[e] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, cs1)));
+            __syncthreads();
+            if (a.rope) {
+                sn4 = *(const f32x4 *)(sin_lds + 4 * j);   // pairs 4j..4j+3
+                cs4 = *(const f32x4 *)(cos_lds + 4 * j);
             }
         }
 #pragma unroll
         for (int g = 0; g < kGroups; g++) {
             if (g0 + 16 * g >= H) break;   // wave-uniform
+            if (__builtin_amdgcn_ballot_w64(kind[g] < 3) == 0) continue;   // no row of this token here
             float y0[4], y1[4];
             // rms_norm: the row's sum of squares (float products) in double
             double ss = 0.0;
@@ -120,19 +159,18 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const NormRopeArgs a)
                 ss += (double)(y0[e] * y0[e]);
                 ss += (double)(y1[e] * y1[e]);
             }
-#pragma unroll
-            for (int off = 8; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+            ss = row16_sum(ss);
             const int kd = kind[g];
             if (kd < 2) {
                 const float mean = (float)(ss / 128.0);
                 const float scale = 1.0f / sqrtf(mean + a.eps);
+                const f32x4 w0 = w_lds[32 * kd + j], w1 = w_lds[32 * kd + 16 + j];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const float w0 = kd == 0 ? qw0[e] : kw0[e], w1 = kd == 0 ? qw1[e] : kw1[e];
-                    const float u0 = (y0[e] * scale) * w0, u1 = (y1[e] * scale) * w1;
+                    const float u0 = (y0[e] * scale) * w0[e], u1 = (y1[e] * scale) * w1[e];
                     if (a.rope) {
-                        y0[e] = u0 * cs[e] - u1 * sn[e];
-                        y1[e] = u0 * sn[e] + u1 * cs[e];
+                        y0[e] = u0 * cs4[e] - u1 * sn4[e];
+                        y1[e] = u0 * sn4[e] + u1 * cs4[e];
                     } else {
                         y0[e] = u0;
                         y1[e] = u1;
