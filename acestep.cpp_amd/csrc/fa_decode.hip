@@ -1125,16 +1125,21 @@ fa_decode_reg_kernel(const FaArgs a) {
     // alternate; the loads of the next block are issued unconditionally
     // before the current block is computed, so the compiler's wait for the
     // current image leaves them in flight.  Under a dense mask the scan's
-    // loads go out first (at the kernel's start, then Q's), then the first
-    // block from the split start, and Q is converted and the scan reduced
-    // while that block is in flight; it is the right block whenever the live
-    // range starts in the split's first 32 keys, as it does for every live
-    // split of a padding mask, and is loaded again otherwise.  (A second
-    // speculative block measured slower: C5 28.2 against 27.0 us.)
+    // loads go out first (at the kernel's start), then Q's; then the first
+    // block from the split start, and Q is converted (and the scan reduced)
+    // while that block is in flight.  Without a mask the live range is the
+    // split, so that block is always the first one; under a dense mask it is
+    // the right block whenever the live range starts in the split's first 32
+    // keys, as it does for every live split of a padding mask, and is loaded
+    // again otherwise.  (A second speculative block measured slower: C5 28.2
+    // against 27.0 us.)  Under a structured mask the block is loaded after
+    // Q's conversion: loaded early, it made the compiler spill (C5's shape
+    // under a structured mask: 35.1 against 27.4 us).
+    constexpr bool kEarly = MM != kMaskStruct;
     {
         Blk x0, x1;
         const int kb_spec = k0 + 32 * t.wave;
-        if constexpr (kDense) {
+        if constexpr (kEarly) {
             if (kb_spec < k1) load(kb_spec, x0);
         }
         if constexpr (kQ8) q_convert8(qraw, qq, dq);
@@ -1143,7 +1148,7 @@ fa_decode_reg_kernel(const FaArgs a) {
         const int kb0 = k0 + ((lo - k0) & ~31) + 32 * t.wave;
         const int n_blk = (lo < hi && kb0 < hi) ? (hi - kb0 + 32 * kDecWaves - 1) / (32 * kDecWaves) : 0;
         if (n_blk > 0) {
-            if (!kDense || kb0 != kb_spec) load(kb0, x0);
+            if (!kEarly || kb0 != kb_spec) load(kb0, x0);   // (early: kb0 differs under dense masks only)
             for (int n = 0;;) {
                 const int kb = kb0 + 32 * kDecWaves * n;
                 if (n + 1 == n_blk) {
