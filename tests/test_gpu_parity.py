@@ -313,6 +313,38 @@ def test_q8_0_broadcast_softcap_alibi(mx):
     check(mx, c, "q8_0 alibi")
 
 
+@pytest.mark.parametrize("kw", [
+    dict(B=2, Sq=150, Nh=8, Nkv=2, Skv=300, mask="random"),
+    dict(B=1, Sq=300, Nh=8, Nkv=2, Skv=516, mask="causal"),
+    dict(B=2, Sq=64, Nh=4, Nkv=4, Skv=129, mask=None, q_layout="contig"),
+    dict(B=4, Bk=1, Sq=96, Nh=8, Nkv=2, Skv=260, mask="random", mask_heads=8),
+    dict(B=1, Sq=130, Nh=16, Nkv=4, Skv=332, mask="random", softcap=30.0),
+    dict(B=1, Sq=70, Nh=16, Nkv=4, Skv=188, mask="random", max_bias=8.0),
+])
+def test_q8_0_prefill(mx, kw):
+    """Sq >= 64 over a Q8_0 cache: Q (quantised to Q8_0 as ggml does) and
+    the K/V rows are staged in F16 and the MFMA prefill kernel runs on them
+    (the launch counts show the route).  Key counts that end a 32-key block
+    early (129, 188, 260, 300, 332, 516; a multiple of 4 where there is a
+    mask, whose rows the prefill reads 8-byte aligned), masks broadcast per
+    head, K/V broadcast over batches, softcap and ALiBi."""
+    import torch
+
+    c = _rand_case(700 + kw["Sq"] + kw["Skv"], kv_type=8, **kw)
+    mx.timing_reset()
+    mx.timing_enable(1)
+    try:
+        check(mx, c, f"q8_0 prefill {kw}")
+        torch.cuda.synchronize()
+        n_stage = mx.timing_read("q8_stage")[1]
+        n_prefill = mx.timing_read("fa_prefill")[1]
+        n_decode = mx.timing_read("fa_decode")[1]
+    finally:
+        mx.timing_enable(False)
+        mx.timing_reset()
+    assert n_stage >= 1 and n_prefill >= 1 and n_decode == 0, (n_stage, n_prefill, n_decode)
+
+
 def test_unaligned_and_short_masks(mx):
     """Mask rows that are only 2-byte aligned (scalar mask reads) and masks
     shorter than one 16-key DMA block take the register-streaming kernel."""

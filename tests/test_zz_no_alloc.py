@@ -63,6 +63,18 @@ def test_noalloc_prefill_matches_workspace_entry(mx):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (label, float(np.abs(got - ref).max()))
 
 
+def test_noalloc_q8_0_prefill_matches_workspace_entry(mx):
+    """Prefill over a Q8_0 cache (tile classes and the F16 staging of Q, K
+    and V in the scratch): two calls, the second smaller."""
+    from test_gpu_parity import _rand_case
+
+    for label, case in (("q8-300", _rand_case(811, B=2, Sq=300, Nh=8, Nkv=2, Skv=516, kv_type=8, mask="causal")),
+                        ("q8-96", _rand_case(812, B=1, Sq=96, Nh=8, Nkv=2, Skv=188, kv_type=8))):
+        print(f"[noalloc] q8_0 prefill {label}: q{tuple(case.q.ne)} k{tuple(case.k.ne)}", flush=True)
+        got, ref = _both(mx, case)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (label, float(np.abs(got - ref).max()))
+
+
 def test_noalloc_allocates_nothing_in_the_engine(mx):
     """The engine's own workspaces do not grow for allocation-free calls."""
     import torch
