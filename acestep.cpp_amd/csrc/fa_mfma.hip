@@ -158,9 +158,10 @@ __device__ __forceinline__ float sum_pair32(float x) {
 // into the instances that need it, so it costs the common path no registers).
 // SM: structured mask (a.sm_*): tile classes and per-element liveness are
 // arithmetic on (query row, key) -- no classifier pass, no mask reads.
-template <int T, bool CAP, bool SM>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-fa_prefill_kernel(const FaArgs a) {
+// QQ8: Q quantised to Q8_0 on load, as ggml quantises Q for a Q8_0 K (the
+// K/V rows of a Q8_0 cache are staged in F16 by q8_stage.hip first).
+template <int T, bool CAP, bool SM, bool QQ8>
+__device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
     using MF = Mfma32<T>;
     using V8 = typename MF::v8;
     static_assert(kD == 128, "kernel is written for D = 128");
@@ -324,6 +325,36 @@ fa_prefill_kernel(const FaArgs a) {
                 u16x8 x = {0, 0, 0, 0, 0, 0, 0, 0};
                 if (row_ok) x = *(const u16x8 *)(qh + 16 * t + 8 * h);
                 qb[t] = __builtin_bit_cast(V8, x);
+            }
+        } else if constexpr (QQ8) {
+            // Q8_0 block bb = dims 32bb .. 32bb+31 = dim-steps 2bb, 2bb+1 of
+            // both halves (this lane and lane ^ 32, the same query row):
+            // d = fp16(amax / 127), q = rint(x * 127 / amax), operand
+            // T(q * d), the product exact in F32
+            const float *qp = (const float *)qrow_p;
+#pragma unroll
+            for (int bb = 0; bb < 4; bb++) {
+                f32x4 x[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) x[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (row_ok) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) x[i] = *(const f32x4 *)(qp + 32 * bb + 16 * (i >> 1) + 8 * h + 4 * (i & 1));
+                }
+                float amax = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) amax = fmaxf(amax, fabsf(x[i][e]));
+                amax = fmaxf(amax, __shfl_xor(amax, 32));
+                const float d = (float)(_Float16)(amax / 127.0f);
+                const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) x[i][e] = (float)(int)__builtin_rintf(x[i][e] * id) * d;
+                qb[2 * bb] = __builtin_bit_cast(V8, cvt8<T>(x[0], x[1]));
+                qb[2 * bb + 1] = __builtin_bit_cast(V8, cvt8<T>(x[2], x[3]));
             }
         } else {
             const float *qp = (const float *)qrow_p;
@@ -593,6 +624,19 @@ fa_prefill_kernel(const FaArgs a) {
     }
 }
 
+template <int T, bool CAP, bool SM>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+fa_prefill_kernel(const FaArgs a) {
+    fa_prefill_body<T, CAP, SM, false>(a);
+}
+
+// Prefill over a Q8_0 cache: K/V rows staged in F16, Q quantised on load.
+template <bool CAP, bool SM>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+fa_prefill_q8q_kernel(const FaArgs a) {
+    fa_prefill_body<T_F16, CAP, SM, true>(a);
+}
+
 hipError_t launch_mask_classify(const FaArgs &a, int n_planes, uint8_t *classes, hipStream_t stream) {
     dim3 grid(a.n_kt, a.n_qt, n_planes);
     hipLaunchKernelGGL(mask_classify_kernel, grid, dim3(256), 0, stream, a, classes);
@@ -609,6 +653,11 @@ hipError_t launch_fa_prefill(const FaArgs &a, int ktype, hipStream_t stream) {
     } else if (ktype == T_BF16) {
         if (sm) { if (cap) MXFA_PF(T_BF16, true, true); else MXFA_PF(T_BF16, false, true); }
         else { if (cap) MXFA_PF(T_BF16, true, false); else MXFA_PF(T_BF16, false, false); }
+    } else if (ktype == T_Q8_0) {
+#define MXFA_PFQ(C, S) hipLaunchKernelGGL((fa_prefill_q8q_kernel<C, S>), grid, dim3(256), kPfLds, stream, a)
+        if (sm) { if (cap) MXFA_PFQ(true, true); else MXFA_PFQ(false, true); }
+        else { if (cap) MXFA_PFQ(true, false); else MXFA_PFQ(false, false); }
+#undef MXFA_PFQ
     } else {
         return hipErrorInvalidValue;
     }

@@ -272,8 +272,8 @@ struct Plan {
     int n_planes = 0;
     size_t ws_bytes = 0;
     int64_t n_tickets = 0;
-    // prefill over a Q8_0 cache: Q and K/V staged in F16 in the workspace,
-    // after the tile classes (stage.qs/ks/vs are workspace offsets until run)
+    // prefill over a Q8_0 cache: K/V staged in F16 in the workspace, after
+    // the tile classes (stage.ks/vs are set in run)
     bool q8_stage = false;
     Q8StageArgs stage{};
     size_t stage_off = 0;
@@ -449,13 +449,13 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     // the prefill kernel addresses one (batch, kv head)'s K and V rows with
     // 32-bit offsets from a buffer base: every row of every key tile must
     // lie within 4 GiB of it
-    // A Q8_0 cache goes to the prefill kernel through F16 staging
+    // A Q8_0 cache goes to the prefill kernel through F16 staging of K/V
     // (q8_stage.hip): contiguous rows of 256 bytes.
     const bool q8 = k->type == MXFA_TYPE_Q8_0;
     const uint64_t row_bytes = q8 ? 256 : (uint64_t)std::max(k->nb[1], v->nb[1]);
     const bool offsets_32 = (uint64_t)n_kt * kPfBN * row_bytes <= 0xFFFFFFFFull;
-    const int64_t n_q_rows = (int64_t)a.Sq * a.Nh * a.B, n_kv_rows = k->ne[1] * k->ne[2] * k->ne[3];
-    const bool stage_ok = !q8 || 16 * (2 * n_kv_rows + n_q_rows) < ((int64_t)1 << 31);
+    const int64_t n_kv_rows = k->ne[1] * k->ne[2] * k->ne[3];
+    const bool stage_ok = !q8 || 32 * n_kv_rows < ((int64_t)1 << 31);
     pl.prefill = (k->type == MXFA_TYPE_F16 || k->type == MXFA_TYPE_BF16 || q8) && a.Sq >= kPrefillMinSq &&
                  mask_vec_ok && offsets_32 && stage_ok && (!mask || n_kt <= kPfMaxKeyTiles);
     if (pl.prefill) {
@@ -468,24 +468,18 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
         a.chunk = a.Skv;
         if (q8) {
             Q8StageArgs &st = pl.stage;
-            st.q = a.q; st.k = a.k; st.v = a.v;
-            st.q_nb1 = a.q_nb1; st.q_nb2 = a.q_nb2; st.q_nb3 = a.q_nb3;
+            st.k = a.k; st.v = a.v;
             st.k_nb1 = a.k_nb1; st.k_nb2 = a.k_nb2; st.k_nb3 = a.k_nb3;
             st.v_nb1 = a.v_nb1; st.v_nb2 = a.v_nb2; st.v_nb3 = a.v_nb3;
-            st.Sq = (uint32_t)a.Sq; st.Nh = (uint32_t)a.Nh;
             st.Skv = (uint32_t)a.Skv; st.Nkv = (uint32_t)a.Nkv;
-            st.n_q = (uint32_t)n_q_rows; st.n_kv = (uint32_t)n_kv_rows;
+            st.n_kv = (uint32_t)n_kv_rows;   // (Q: quantised to Q8_0 by the prefill kernel on load)
             pl.q8_stage = true;
             pl.stage_off = (pl.ws_bytes + 255) & ~(size_t)255;
-            pl.ws_bytes = pl.stage_off + 256 * (size_t)(n_q_rows + 2 * n_kv_rows);
-            // the prefill reads the staged F16 rows: Q [128, Sq, Nh, B],
-            // K and V [128, Skv, Nkv, Bk]
-            a.q16 = 1;
-            a.q_nb1 = 256; a.q_nb2 = 256 * (int64_t)a.Sq; a.q_nb3 = a.q_nb2 * a.Nh;
+            pl.ws_bytes = pl.stage_off + 256 * (size_t)(2 * n_kv_rows);
+            // the prefill reads the staged F16 K and V rows [128, Skv, Nkv, Bk]
             a.k_nb1 = a.v_nb1 = 256;
             a.k_nb2 = a.v_nb2 = 256 * (int64_t)a.Skv;
             a.k_nb3 = a.v_nb3 = a.k_nb2 * a.Nkv;
-            pl.ktype = MXFA_TYPE_F16;
         }
         return;
     }
@@ -728,10 +722,8 @@ int run(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const 
         if (pl.q8_stage) {
             char *base = (char *)ws + pl.stage_off;
             Q8StageArgs &st = pl.stage;
-            st.qs = base;
-            st.ks = st.qs + 256 * (size_t)st.n_q;
+            st.ks = base;
             st.vs = st.ks + 256 * (size_t)st.n_kv;
-            a.q = st.qs;
             a.k = st.ks;
             a.v = st.vs;
             e = timed_launch("q8_stage", stream, [&] { return launch_q8_stage(st, stream); });

@@ -26,20 +26,20 @@ constexpr int kPfBN = 64;    // keys per K/V tile
 constexpr int kPfMaxKeyTiles = 512;   // class rows held in two registers per lane
 hipError_t launch_mask_classify(const FaArgs &a, int n_planes, uint8_t *classes, hipStream_t stream);
 
-// MFMA prefill / DiT kernel.  ktype: T_F16/T_BF16.
+// MFMA prefill / DiT kernel.  ktype: T_F16/T_BF16, or T_Q8_0 for K/V
+// staged in F16 by launch_q8_stage (Q, F32, quantised to Q8_0 on load).
 hipError_t launch_fa_prefill(const FaArgs &a, int ktype, hipStream_t stream);
 
-// F16 staging of a prefill over a Q8_0 cache (q8_stage.hip): Q (F32, as
-// ggml quantises it to Q8_0) and the Q8_0 K/V rows, dequantised, into
-// contiguous [128, Sq, Nh, B] and [128, Skv, Nkv, Bk] F16 buffers.
-// K and V have the same shape; K/V rows 4-byte aligned, Q rows 16-byte;
-// 16 * (2 n_kv + n_q) < 2^31.
+// F16 staging of a prefill over a Q8_0 cache (q8_stage.hip): the Q8_0 K/V
+// rows, dequantised, into contiguous [128, Skv, Nkv, Bk] F16 buffers (the
+// prefill kernel quantises Q itself: launch_fa_prefill with T_Q8_0).  K and
+// V have the same shape, rows 4-byte aligned; 32 n_kv < 2^31.
 struct Q8StageArgs {
-    const char *q, *k, *v;
-    int64_t q_nb1, q_nb2, q_nb3, k_nb1, k_nb2, k_nb3, v_nb1, v_nb2, v_nb3;
-    char *qs, *ks, *vs;
-    uint32_t Sq, Nh, Skv, Nkv;
-    uint32_t n_q, n_kv;   // staged Q rows (Sq Nh B), K rows = V rows (Skv Nkv Bk)
+    const char *k, *v;
+    int64_t k_nb1, k_nb2, k_nb3, v_nb1, v_nb2, v_nb3;
+    char *ks, *vs;
+    uint32_t Skv, Nkv;
+    uint32_t n_kv;   // K rows = V rows (Skv Nkv Bk)
 };
 hipError_t launch_q8_stage(const Q8StageArgs &a, hipStream_t stream);
 

@@ -1,4 +1,4 @@
-// q8_stage.hip -- the operands of a prefill over a Q8_0 KV cache, staged in
+// q8_stage.hip -- the K/V rows of a prefill over a Q8_0 KV cache, staged in
 // F16 for the MFMA prefill kernel.
 //
 // ggml's CPU flash_attn_ext over a Q8_0 cache
@@ -8,38 +8,31 @@
 // d_q d_k; V rows are dequantised to F32 (q * d) and accumulated in F32.
 // The reference reaches it from src/qwen3-lm.h's prompt path over a Q8_0
 // cache (a prompt continued at kv_pos > 0).  This pass writes
-//   Q' = f16(q_q * d_q)   with (q_q, d_q) as ggml's quantize_row_q8_0 forms
-//                         them: d_q = fp16(amax / 127), q_q = rint(x * 127 / amax);
 //   K' = f16(q_k * d_k),  V' = f16(q_v * d_v)
-// each product exact in F32 (8-bit times 11-bit) and rounded once to F16.
-// The prefill kernel's F16 products of Q' and K' are exact in its F32
-// accumulators, so the scores differ from ggml's integer dots only by the
-// two F16 roundings (relative 2^-11 per factor), and P V by V's rounding,
-// as in the decode kernel, which dequantises V to F16 the same way.
-// Values beyond F16's range (|q d| > 65504) become infinite.
+// each product exact in F32 (8-bit times 11-bit) and rounded once to F16;
+// the prefill kernel quantises Q to Q8_0 on load as ggml does and uses
+// Q' = f16(q_q * d_q) (fa_prefill_q8q_kernel).  Its F16 products of Q' and
+// K' are exact in its F32 accumulators, so the scores differ from ggml's
+// integer dots only by the two F16 roundings (relative 2^-11 per factor),
+// and P V by V's rounding, as in the decode kernel, which dequantises V to
+// F16 the same way.  Values beyond F16's range (|q d| > 65504) become
+// infinite.
 //
 // One thread writes 8 values (16 bytes) of one staged row: 16 threads per
-// row of 128.  Rows [0, n_kv) are K rows, [n_kv, 2 n_kv) V rows, then Q rows.
+// row of 128.  Rows [0, n_kv) are K rows, [n_kv, 2 n_kv) V rows.
 
 #include "mxfa_common.h"
 #include "mxfa_internal.h"
 
 namespace mxfa {
 
-template <int CTRL>
-__device__ __forceinline__ float quad_max(float v) {
-    return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
-                                                                       false)));
-}
-
 __global__ void __launch_bounds__(256) q8_stage_kernel(const Q8StageArgs a) {
     const uint32_t t = blockIdx.x * 256u + threadIdx.x;
     const uint32_t row = t >> 4, j = t & 15;   // staged row, 8-value chunk
-    // (whole rows, so the 4 lanes of a Q8_0 block stay together)
-    if (row >= 2 * a.n_kv + a.n_q) return;
+    if (row >= 2 * a.n_kv) return;
     float y[8];
     char *dst;
-    if (row < 2 * a.n_kv) {
+    {
         const bool is_v = row >= a.n_kv;
         const uint32_t r = is_v ? row - a.n_kv : row;
         const uint32_t key = r % a.Skv, rest = r / a.Skv, kvh = rest % a.Nkv, bk = rest / a.Nkv;
@@ -65,26 +58,6 @@ __global__ void __launch_bounds__(256) q8_stage_kernel(const Q8StageArgs a) {
             y[4 + e] = (float)(int8_t)(hi >> (8 * e)) * d;
         }
         dst = (is_v ? a.vs : a.ks) + (int64_t)r * 256 + 16 * j;
-    } else {
-        const uint32_t r = row - 2 * a.n_kv;
-        const uint32_t iq1 = r % a.Sq, rest = r / a.Sq, head = rest % a.Nh, b = rest / a.Nh;
-        const float *qp = (const float *)(a.q + (int64_t)iq1 * a.q_nb1 + (int64_t)head * a.q_nb2 +
-                                          (int64_t)b * a.q_nb3) + 8 * j;
-        const f32x4 x0 = *(const f32x4 *)qp, x1 = *(const f32x4 *)(qp + 4);
-        // Q8_0 block = 32 values = the 4 lanes of a quad
-        float amax = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 4; e++) amax = fmaxf(amax, fmaxf(fabsf(x0[e]), fabsf(x1[e])));
-        amax = quad_max<0xB1>(amax);   // quad_perm [1, 0, 3, 2]
-        amax = quad_max<0x4E>(amax);   // quad_perm [2, 3, 0, 1]
-        const float d = (float)(_Float16)(amax / 127.0f);
-        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            y[e] = (float)(int)__builtin_rintf(x0[e] * id) * d;
-            y[4 + e] = (float)(int)__builtin_rintf(x1[e] * id) * d;
-        }
-        dst = a.qs + (int64_t)r * 256 + 16 * j;
     }
     u32x4 w;
 #pragma unroll
@@ -96,7 +69,7 @@ __global__ void __launch_bounds__(256) q8_stage_kernel(const Q8StageArgs a) {
 }
 
 hipError_t launch_q8_stage(const Q8StageArgs &a, hipStream_t stream) {
-    const int64_t threads = 16 * ((int64_t)2 * a.n_kv + a.n_q);
+    const int64_t threads = 16 * (int64_t)2 * a.n_kv;
     if (threads <= 0) return hipSuccess;
     if (threads >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(q8_stage_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, a);

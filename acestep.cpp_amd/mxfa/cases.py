@@ -310,8 +310,29 @@ def c4_cross8(**kw) -> FaCase:
     return dit_cross("c4x8", seed=SEEDS["c4x"], Nkv=8, **kw)
 
 
+def c2_q8(n_tokens=2048, **kw) -> FaCase:
+    """C2's prompt over a Q8_0 cache (the prompt path of qwen3-lm.h with a
+    Q8_0 cache type): the same Q, mask and N(0,1) K/V rows as C2, the K/V
+    rows quantised to Q8_0 (rows of 128 = 4 blocks of 34 B)."""
+    base = c2(n_tokens=n_tokens, **kw)
+    m = base.meta
+    Nkv, max_seq, kv_len, seed = m["Nkv"], m["max_seq"], m["kv_len"], m["seed"]
+    row = D // 32 * 34
+    bufs = []
+    for stream in (synth.STREAM_K, synth.STREAM_V):
+        f = np.zeros(Nkv * max_seq * D, dtype=np.float32)
+        for g in range(Nkv):
+            st = D * max_seq * g
+            f[st:st + D * kv_len] = synth.normal(seed, stream, st, D * kv_len)
+        bufs.append(quantize_q8_0(f))
+    kvnb = (34, row, row * max_seq, row * max_seq * Nkv)
+    k = HostView(TYPE_Q8_0, base.k.ne, kvnb, bufs[0])
+    v = HostView(TYPE_Q8_0, base.v.ne, kvnb, bufs[1])
+    return FaCase("c2q8", base.q, k, v, base.mask, base.scale, meta=dict(m, kind="lm_single_q8"))
+
+
 BUILDERS = {"c1": c1, "c2": c2, "c3": c3, "c4s": c4_self, "c4x": c4_cross, "c5": c5, "c4s8": c4_self8,
-            "c4x8": c4_cross8}
+            "c4x8": c4_cross8, "c2q8": c2_q8}
 
 
 def with_q16(case: FaCase) -> FaCase:

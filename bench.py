@@ -85,14 +85,16 @@ DESCR.update({
     "nrx": "pre-attention step of C4 cross (mxfa_qk_norm_rope, no RoPE): QK-RMSNorm + F16 cast of B=2 x (3000 "
            "tokens x 16 Q heads + 256 encoder tokens x 16 K + 16 V heads)",
     "c4xq": "C4 cross with Q in F16 as the cross pre-attention step writes it",
+    "c2q8": "C2 over a Q8_0 KV cache (K/V rows quantised from the same N(0,1) data): Q and K/V staged in F16, "
+            "then the MFMA prefill kernel",
     "stream": "calibration, not an engine op: one streaming read of 1 GiB with 16-byte loads "
               "(libmxfa_calib.so), the HBM rate a plain read reaches on this box",
 })
 BOUND = {"c1": "hbm", "c2": "mfma", "c3": "hbm", "c4s": "mfma", "c4x": "hbm", "c5": "hbm", "c4s8": "mfma", "c4x8": "hbm",
-         "c2m": "mfma", "c3m": "hbm", "c4xm": "hbm", "c2q": "mfma", "c4xq": "hbm"}
+         "c2m": "mfma", "c3m": "hbm", "c4xm": "hbm", "c2q": "mfma", "c4xq": "hbm", "c2q8": "mfma"}
 KERNEL = {"c1": "fa_decode", "c2": "fa_prefill", "c3": "fa_decode", "c4s": "fa_prefill", "c4x": "fa_prefill",
           "c5": "fa_decode", "c4s8": "fa_prefill", "c4x8": "fa_prefill", "c2m": "fa_prefill", "c3m": "fa_decode", "c4xm": "fa_prefill", "c2q": "fa_prefill",
-          "c4xq": "fa_prefill"}
+          "c4xq": "fa_prefill", "c2q8": "fa_prefill"}
 STRUCTURED = {"c2m": "c2", "c3m": "c3", "c4xm": "c4x"}   # structured-mask variant -> dense config
 
 
@@ -185,7 +187,7 @@ def time_case(mx, torch, case, steps, warmup, rotate_bytes=None, spec=None):
     torch.cuda.synchronize()
     mx.timing_enable(False)
     rep = {}
-    for fam in ("fa_prefill", "mask_classify", "fa_decode"):
+    for fam in ("fa_prefill", "mask_classify", "fa_decode", "q8_stage"):
         tot, n = mx.timing_read(fam)
         if n:
             rep[fam] = tot / n
@@ -635,7 +637,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c4s8,c4x8,c2m,c3m,c4xm,c2q,c4xq,kw2,kw3,kw5,nr2,nrx,dstep,dstepf,stream")
+    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c4s8,c4x8,c2m,c3m,c4xm,c2q,c4xq,c2q8,kw2,kw3,kw5,nr2,nrx,dstep,dstepf,"
+                    "stream")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB copy (counter calibration under rocprofv3)")
