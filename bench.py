@@ -26,7 +26,8 @@ the KV-cache writes that precede C2 / C3 (GGML_OP_SET_ROWS:
 kw2, kw3, and kw5 into a Q8_0 cache; GB/s of F32 read + converted row
 written + row ids, vs the HBM peak), the fused pre-attention step of C2
 (nr2: QK-RMSNorm + RoPE + F16 cast + cache write, GB/s vs the HBM peak) and
-C2's attention on the F16 Q that step writes (c2q).  Inputs of bandwidth-bound configs are rotated over enough device
+C2's attention on the F16 Q that step writes (c2q), and C2 over a Q8_0 cache (c2q8: K/V staged in F16,
+then the MFMA prefill).  Inputs of bandwidth-bound configs are rotated over enough device
 copies that consecutive steps do not hit in the 256 MB Infinity Cache.  "stream" is a calibration, not an
 engine op: a plain 1 GiB streaming read (libmxfa_calib.so), the HBM rate the decode figures compare with.
 Each config first runs untimed for SETTLE_S seconds (the GPU clock rises under sustained load and settles
