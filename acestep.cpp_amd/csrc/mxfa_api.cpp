@@ -46,6 +46,18 @@ int fail(int code, const char *fmt, ...) {
     return code;
 }
 
+// One dense mask's tile classes within a graph (mxfa_graph_begin): the
+// classes depend only on the mask's bytes inside [0, Skv) x [0, Sq) of each
+// plane, so (data, ne, nb, Sq, Skv) identifies them while the mask's
+// contents stay fixed, as they do during one ggml graph computation.
+struct ClassEntry {
+    const void *data = nullptr;
+    int64_t ne[4] = {0, 0, 0, 0};
+    size_t nb[4] = {0, 0, 0, 0};
+    int64_t Sq = 0, Skv = 0;
+    uint8_t *cls = nullptr;
+};
+
 struct Workspace {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -54,6 +66,12 @@ struct Workspace {
     int *tickets = nullptr;   // zero between calls
     int64_t n_tickets = 0;
     std::vector<void *> retired;   // outgrown buffers, freed by mxfa_release()
+    // mask tile classes of the current graph: epoch 0 = no graph begun on
+    // this stream (every call classifies its own mask into `ptr`)
+    uint64_t epoch = 0;
+    uint8_t *arena = nullptr;
+    size_t arena_size = 0, arena_used = 0;
+    std::vector<ClassEntry> entries;
 };
 std::mutex g_ws_mu;
 std::vector<Workspace> g_ws;  // one per (device, stream) that has needed one
@@ -540,24 +558,90 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     }
 }
 
+// Workspace of (current device, stream), created on first use (g_ws_mu held).
+int workspace_of(hipStream_t stream, Workspace **out) {
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(MXFA_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    for (Workspace &w : g_ws)
+        if (w.device == dev && w.stream == stream) {
+            *out = &w;
+            return MXFA_OK;
+        }
+    g_ws.push_back(Workspace{});
+    g_ws.back().device = dev;
+    g_ws.back().stream = stream;
+    *out = &g_ws.back();
+    return MXFA_OK;
+}
+
+// Tile classes of a dense mask within the stream's current graph.  Sets
+// *cls to NULL when no graph has begun on the stream (the call classifies
+// into its workspace as before); else to the mask's class bytes in the
+// stream's arena, with *fresh = true when this call is the mask's first use
+// in the graph (it must run the classifier) and false when an earlier node
+// of the graph already did.  The arena grows (the old one is retired, as
+// workspaces are) except under capture.
+int graph_classes(const mxfa_tensor *mask, int64_t Sq, int64_t Skv, size_t bytes, hipStream_t stream, uint8_t **cls,
+                  bool *fresh) {
+    *cls = nullptr;
+    *fresh = false;
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    Workspace *w = nullptr;
+    const int rc = workspace_of(stream, &w);
+    if (rc != MXFA_OK) return rc;
+    if (w->epoch == 0) return MXFA_OK;
+    for (const ClassEntry &c : w->entries) {
+        bool same = c.data == mask->data && c.Sq == Sq && c.Skv == Skv;
+        for (int i = 0; i < 4 && same; i++) same = c.ne[i] == mask->ne[i] && c.nb[i] == mask->nb[i];
+        if (same) {
+            *cls = c.cls;
+            return MXFA_OK;
+        }
+    }
+    const size_t need = (w->arena_used + bytes + 255) & ~(size_t)255;
+    if (need > w->arena_size) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return fail(MXFA_ERR_UNSUPPORTED,
+                        "the graph's mask class arena must grow (%zu bytes) while the stream is being captured; "
+                        "compute the graph once eagerly before capturing it",
+                        need);
+        const size_t want = std::max<size_t>((size_t)64 << 10, 2 * need);
+        void *p = nullptr;
+        const hipError_t e = hipMalloc(&p, want);
+        if (e != hipSuccess) return fail(MXFA_ERR_NOMEM, "hipMalloc(%zu): %s", want, hipGetErrorString(e));
+        if (w->arena) w->retired.push_back(w->arena);
+        w->arena = (uint8_t *)p;
+        w->arena_size = want;
+        w->arena_used = 0;   // (entries of this graph keep their bytes in the retired arena)
+    }
+    ClassEntry c;
+    c.data = mask->data;
+    for (int i = 0; i < 4; i++) {
+        c.ne[i] = mask->ne[i];
+        c.nb[i] = mask->nb[i];
+    }
+    c.Sq = Sq;
+    c.Skv = Skv;
+    c.cls = w->arena + w->arena_used;
+    w->arena_used = (w->arena_used + bytes + 255) & ~(size_t)255;
+    w->entries.push_back(c);
+    *cls = c.cls;
+    *fresh = true;
+    return MXFA_OK;
+}
+
 int ensure_workspace(size_t bytes, int64_t n_tickets, hipStream_t stream, void **out, int **tickets) {
     *out = nullptr;
     *tickets = nullptr;
     if (bytes == 0 && n_tickets == 0) return MXFA_OK;
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return fail(MXFA_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
     std::lock_guard<std::mutex> lock(g_ws_mu);
     Workspace *found = nullptr;
-    for (Workspace &w : g_ws)
-        if (w.device == dev && w.stream == stream) found = &w;
-    if (!found) {
-        g_ws.push_back(Workspace{});
-        found = &g_ws.back();
-        found->device = dev;
-        found->stream = stream;
-    }
+    const int rc = workspace_of(stream, &found);
+    if (rc != MXFA_OK) return rc;
     Workspace &ws = *found;
+    hipError_t e;
     if (ws.size < bytes || ws.n_tickets < n_tickets) {
         // Growing allocates, which a stream under HIP graph capture cannot
         // do: the first call of a shape must run eagerly (or through
@@ -730,11 +814,24 @@ int run(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const 
             if (e != hipSuccess) return fail(MXFA_ERR_HIP, "q8 stage launch: %s", hipGetErrorString(e));
         }
         if (a.mask) {
+            // within a graph (mxfa_graph_begin) a mask is classified at its
+            // first node only; otherwise every call classifies its own
             uint8_t *cls = (uint8_t *)ws;
+            bool classify = true;
+            if (!fixed) {
+                uint8_t *gc = nullptr;
+                const int rc = graph_classes(mask, a.Sq, a.Skv, (size_t)pl.n_planes * a.n_qt * a.n_kt_pad, stream,
+                                             &gc, &classify);
+                if (rc != MXFA_OK) return rc;
+                if (gc) cls = gc;
+                else classify = true;
+            }
             a.tile_class = cls;
-            e = timed_launch("mask_classify", stream,
-                             [&] { return launch_mask_classify(a, pl.n_planes, cls, stream); });
-            if (e != hipSuccess) return fail(MXFA_ERR_HIP, "mask classify launch: %s", hipGetErrorString(e));
+            if (classify) {
+                e = timed_launch("mask_classify", stream,
+                                 [&] { return launch_mask_classify(a, pl.n_planes, cls, stream); });
+                if (e != hipSuccess) return fail(MXFA_ERR_HIP, "mask classify launch: %s", hipGetErrorString(e));
+            }
         }
         e = timed_launch("fa_prefill", stream, [&] { return launch_fa_prefill(a, pl.ktype, stream); });
         if (e != hipSuccess) return fail(MXFA_ERR_HIP, "prefill launch: %s", hipGetErrorString(e));
@@ -829,6 +926,28 @@ int mxfa_reserve(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *
     return ensure_workspace(pl.ws_bytes, pl.n_tickets, (hipStream_t)hip_stream, &ws, &tickets);
 }
 
+int mxfa_graph_begin(void *hip_stream) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    Workspace *w = nullptr;
+    const int rc = workspace_of((hipStream_t)hip_stream, &w);
+    if (rc != MXFA_OK) return rc;
+    w->epoch++;
+    w->arena_used = 0;
+    w->entries.clear();
+    return MXFA_OK;
+}
+
+int mxfa_graph_end(void *hip_stream) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    Workspace *w = nullptr;
+    const int rc = workspace_of((hipStream_t)hip_stream, &w);
+    if (rc != MXFA_OK) return rc;
+    w->epoch = 0;
+    w->arena_used = 0;
+    w->entries.clear();
+    return MXFA_OK;
+}
+
 int mxfa_supports_masked(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_mask_spec *mask,
                          const mxfa_params *params, const mxfa_tensor *dst) {
     if (check(q, k, v, nullptr, params, dst) != MXFA_OK || check_spec(mask, q) != MXFA_OK) return 0;
@@ -901,6 +1020,7 @@ void mxfa_release(void) {
         (void)hipDeviceSynchronize();
         if (w.ptr) (void)hipFree(w.ptr);
         if (w.tickets) (void)hipFree(w.tickets);
+        if (w.arena) (void)hipFree(w.arena);
         for (void *p : w.retired) (void)hipFree(p);
     }
     g_ws.clear();
@@ -912,7 +1032,7 @@ int mxfa_workspace_info(int64_t *live_bytes, int64_t *retired_buffers) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
     int64_t live = 0, ret = 0;
     for (const Workspace &w : g_ws) {
-        live += (int64_t)w.size + w.n_tickets * (int64_t)sizeof(int);
+        live += (int64_t)w.size + w.n_tickets * (int64_t)sizeof(int) + (int64_t)w.arena_size;
         ret += (int64_t)w.retired.size();
     }
     *live_bytes = live;

@@ -18,6 +18,7 @@ without it raises.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 from dataclasses import dataclass
@@ -42,6 +43,8 @@ EXPORTED_SYMBOLS = (
     "mxfa_flash_attn_ext_masked",
     "mxfa_flash_attn_ext_noalloc",
     "mxfa_reserve",
+    "mxfa_graph_begin",
+    "mxfa_graph_end",
     "mxfa_qk_norm_rope",
     "mxfa_qk_norm_rope_supports",
     "mxfa_set_rows_supports",
@@ -157,6 +160,10 @@ def _load():
     L.mxfa_qk_norm_rope_supports.restype = ctypes.c_int
     L.mxfa_reserve.argtypes = [P, P, P, P, ctypes.POINTER(MxfaParams), ctypes.c_void_p]
     L.mxfa_reserve.restype = ctypes.c_int
+    L.mxfa_graph_begin.argtypes = [ctypes.c_void_p]
+    L.mxfa_graph_begin.restype = ctypes.c_int
+    L.mxfa_graph_end.argtypes = [ctypes.c_void_p]
+    L.mxfa_graph_end.restype = ctypes.c_int
     L.mxfa_set_rows_supports.argtypes = [P, P, P]
     L.mxfa_set_rows_supports.restype = ctypes.c_int
     L.mxfa_set_rows.argtypes = [P, P, P, ctypes.c_void_p]
@@ -323,6 +330,42 @@ def reserve(q, k, v, mask, scale, max_bias=0.0, logit_softcap=0.0, prec=PREC_F32
     rc = lib.mxfa_reserve(refs[0], refs[1], refs[2], refs[3], ctypes.byref(p), ctypes.c_void_p(int(stream)))
     if rc != OK:
         raise MxfaError(rc, last_error())
+
+
+def graph_begin(stream=None) -> None:
+    """Starts one graph's computation on `stream` (mxfa_graph_begin): until
+    the next call, FA calls on the stream that share a dense mask (same data
+    pointer, shape and strides, same Sq and Skv) classify it once."""
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.mxfa_graph_begin(ctypes.c_void_p(int(stream)))
+    if rc != OK:
+        raise MxfaError(rc, last_error())
+
+
+def graph_end(stream=None) -> None:
+    """Ends the graph begun on `stream` (mxfa_graph_end): FA calls on it
+    classify their masks per call again."""
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.mxfa_graph_end(ctypes.c_void_p(int(stream)))
+    if rc != OK:
+        raise MxfaError(rc, last_error())
+
+
+@contextlib.contextmanager
+def graph(stream=None):
+    """with mxfa.graph(stream): ... -- the FA calls inside share their
+    masks' classification (mxfa_graph_begin / mxfa_graph_end)."""
+    graph_begin(stream)
+    try:
+        yield
+    finally:
+        graph_end(stream)
 
 
 def set_rows_supports(dst, src, rows) -> bool:

@@ -310,6 +310,19 @@ def c4_cross8(**kw) -> FaCase:
     return dit_cross("c4x8", seed=SEEDS["c4x"], Nkv=8, **kw)
 
 
+def c4_self_window(**kw) -> FaCase:
+    """The DiT's sliding-window self-attention layer at C4's size: every even
+    layer (layer_type 0) reads the window mask sa_mask_sw [S, S, 1, N]
+    (dit-graph.h:522-524, :574-576) built at dit-sampler.h:262-289 with the
+    GGUF's acestep.sliding_window (dit.h:286; 128 in the reference's runs)."""
+    return dit_self("c4sw", seed=SEEDS["c4s"], window=128, **kw)
+
+
+def c4_self_window8(**kw) -> FaCase:
+    """The window layer with the real DiT's 16 / 8 heads."""
+    return dit_self("c4sw8", seed=SEEDS["c4s"], Nkv=8, window=128, **kw)
+
+
 def c2_q8(n_tokens=2048, **kw) -> FaCase:
     """C2's prompt over a Q8_0 cache (the prompt path of qwen3-lm.h with a
     Q8_0 cache type): the same Q, mask and N(0,1) K/V rows as C2, the K/V
@@ -332,7 +345,7 @@ def c2_q8(n_tokens=2048, **kw) -> FaCase:
 
 
 BUILDERS = {"c1": c1, "c2": c2, "c3": c3, "c4s": c4_self, "c4x": c4_cross, "c5": c5, "c4s8": c4_self8,
-            "c4x8": c4_cross8, "c2q8": c2_q8}
+            "c4x8": c4_cross8, "c2q8": c2_q8, "c4sw": c4_self_window, "c4sw8": c4_self_window8}
 
 
 def with_q16(case: FaCase) -> FaCase:

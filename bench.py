@@ -90,13 +90,29 @@ DESCR.update({
             "then the MFMA prefill kernel",
     "stream": "calibration, not an engine op: one streaming read of 1 GiB with 16-byte loads "
               "(libmxfa_calib.so), the HBM rate a plain read reaches on this box",
+    "c4sw": "DiT sliding-window self-attention (the even layers): B=2, 3000 tokens, 16/16 heads, D=128, "
+            "dense F16 window mask [3000, 3000, 1, 2], window 128",
+    "c4sw8": "the window layer with the real DiT's 8 KV heads: B=2, 3000 tokens, 16/8 heads, window 128",
+    "c4swm": "C4 window layer with the window as metadata (mxfa_flash_attn_ext_masked, no mask tensor)",
+    "c4swm8": "the window layer, 16/8 heads, window as metadata",
+    "c2g": "C2 per FA call of a 36-layer Qwen3-4B forward: 36 calls (own Q/K/V each) on one causal mask in one "
+           "graph (mxfa_graph_begin/end), the mask classified once per forward",
+    "c4xg": "C4 cross per FA call of a 24-layer DiT step: 24 calls (own Q/K/V each, rotated) on one padding mask "
+            "in one graph, the mask classified once per step",
+    "c4swg": "C4 window layer per FA call of a DiT step: its 12 window layers on one sa_mask_sw in one graph",
 })
+# configs that time a graph of L calls on one mask: name -> (case, L)
+GRAPHS = {"c2g": ("c2", 36), "c4xg": ("c4x", 24), "c4swg": ("c4sw", 12)}
 BOUND = {"c1": "hbm", "c2": "mfma", "c3": "hbm", "c4s": "mfma", "c4x": "hbm", "c5": "hbm", "c4s8": "mfma", "c4x8": "hbm",
-         "c2m": "mfma", "c3m": "hbm", "c4xm": "hbm", "c2q": "mfma", "c4xq": "hbm", "c2q8": "mfma"}
+         "c2m": "mfma", "c3m": "hbm", "c4xm": "hbm", "c2q": "mfma", "c4xq": "hbm", "c2q8": "mfma",
+         "c4sw": "hbm", "c4sw8": "hbm", "c4swm": "hbm", "c4swm8": "hbm", "c2g": "mfma", "c4xg": "hbm",
+         "c4swg": "hbm"}
 KERNEL = {"c1": "fa_decode", "c2": "fa_prefill", "c3": "fa_decode", "c4s": "fa_prefill", "c4x": "fa_prefill",
           "c5": "fa_decode", "c4s8": "fa_prefill", "c4x8": "fa_prefill", "c2m": "fa_prefill", "c3m": "fa_decode", "c4xm": "fa_prefill", "c2q": "fa_prefill",
-          "c4xq": "fa_prefill", "c2q8": "fa_prefill"}
-STRUCTURED = {"c2m": "c2", "c3m": "c3", "c4xm": "c4x"}   # structured-mask variant -> dense config
+          "c4xq": "fa_prefill", "c2q8": "fa_prefill", "c4sw": "fa_prefill", "c4sw8": "fa_prefill",
+          "c4swm": "fa_prefill", "c4swm8": "fa_prefill", "c2g": "fa_prefill", "c4xg": "fa_prefill",
+          "c4swg": "fa_prefill"}
+STRUCTURED = {"c2m": "c2", "c3m": "c3", "c4xm": "c4x", "c4swm": "c4sw", "c4swm8": "c4sw8"}   # structured-mask variant -> dense config
 
 
 def log(*a):
@@ -130,10 +146,15 @@ def settle(torch, step):
             return i
 
 
-def time_case(mx, torch, case, steps, warmup, rotate_bytes=None, spec=None):
+def time_case(mx, torch, case, steps, warmup, rotate_bytes=None, spec=None, graph_layers=None):
     """Returns (ms per call, per-kernel avg ms dict).  With `spec` (mask_spec
     keyword arguments) the call is the structured-mask entry point and no
-    mask tensor exists; the algorithmic work is that of the dense case."""
+    mask tensor exists; the algorithmic work is that of the dense case.
+    With `graph_layers` L, a step is one graph of L calls (one per layer)
+    bracketed by mxfa_graph_begin / mxfa_graph_end, all reading one mask
+    tensor, as a forward pass of the reference does: the mask is classified
+    once per graph.  Figures are then per call, the classifier's time spread
+    over the graph's L calls."""
     from mxfa import cases as C
 
     w = C.work(case)
@@ -153,14 +174,25 @@ def time_case(mx, torch, case, steps, warmup, rotate_bytes=None, spec=None):
                                   o.data_ptr(), o))
     stream = torch.cuda.current_stream().cuda_stream
 
-    def step(i):
+    def call(i, m=None):
         c = copies[i % n_copies]
         if spec is None:
-            mx.flash_attn_ext(c["q"], c["k"], c["v"], c["m"], case.scale, case.max_bias, case.softcap,
-                              dst=outs[i % n_copies], stream=stream)
+            mx.flash_attn_ext(c["q"], c["k"], c["v"], c["m"] if m is None else m, case.scale, case.max_bias,
+                              case.softcap, dst=outs[i % n_copies], stream=stream)
         else:
             mx.flash_attn_ext_masked(c["q"], c["k"], c["v"], spec_obj, case.scale, case.max_bias, case.softcap,
                                      dst=outs[i % n_copies], stream=stream)
+
+    L = graph_layers or 1
+    if graph_layers:
+        def step(i):
+            # layer l of forward i: its own Q/K/V copy, the forward's one mask
+            mx.graph_begin(stream)
+            for l in range(L):
+                call(i * L + l, copies[0]["m"])
+            mx.graph_end(stream)
+    else:
+        step = call
 
     settle(torch, step)
     for i in range(warmup):
@@ -172,7 +204,7 @@ def time_case(mx, torch, case, steps, warmup, rotate_bytes=None, spec=None):
         step(i)
     ev1.record()
     torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / steps
+    ms = ev0.elapsed_time(ev1) / (steps * L)
     # Per-kernel durations: every launch repeated REPEAT times back to back
     # between one pair of HIP events on its launch stream (mxfa timing mode
     # REPEAT), so the average is the kernel's own time plus the dispatch gap,
@@ -183,7 +215,8 @@ def time_case(mx, torch, case, steps, warmup, rotate_bytes=None, spec=None):
     # pass it is the call time less the classifier's.
     mx.timing_reset()
     mx.timing_enable(REPEAT)
-    for i in range(max(4, steps // REPEAT)):
+    n_timed = max(4, steps // REPEAT)
+    for i in range(n_timed):
         step(i)
     torch.cuda.synchronize()
     mx.timing_enable(False)
@@ -191,7 +224,8 @@ def time_case(mx, torch, case, steps, warmup, rotate_bytes=None, spec=None):
     for fam in ("fa_prefill", "mask_classify", "fa_decode", "q8_stage"):
         tot, n = mx.timing_read(fam)
         if n:
-            rep[fam] = tot / n
+            # (per call: a graph's classifier launches spread over its calls)
+            rep[fam] = tot / n if fam != "mask_classify" or not graph_layers else tot / (n_timed * L * REPEAT)
     mx.timing_reset()
     kern = dict(rep)
     if rotate_bytes is not None:
@@ -638,8 +672,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--only", type=str, default="c1,c2,c3,c4s,c4x,c5,c4s8,c4x8,c2m,c3m,c4xm,c2q,c4xq,c2q8,kw2,kw3,kw5,nr2,nrx,dstep,dstepf,"
-                    "stream")
+    ap.add_argument("--only", type=str, default="c1,c2,c2g,c3,c4s,c4x,c4xg,c5,c4s8,c4x8,c4sw,c4sw8,c4swg,c2m,c3m,c4xm,"
+                    "c4swm,c4swm8,c2q,c4xq,c2q8,kw2,kw3,kw5,nr2,nrx,dstep,dstepf,stream")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB copy (counter calibration under rocprofv3)")
@@ -661,10 +695,11 @@ def main():
 
     torch.cuda.set_device(0)
     names = [n.strip() for n in args.only.split(",") if n.strip()]
-    if "c2" not in names:
-        names.insert(0, "c2")
+    # the headline: C2 as the forward pass runs it (c2g), or C2 per call
+    if "c2g" not in names and "c2" not in names:
+        names.insert(0, "c2g")
     results = {}
-    headline = None
+    headline, headline_name = None, None
     for name in names:
         log(f"[bench] building {name} ...")
         if name in C.SET_ROWS_BUILDERS:
@@ -694,6 +729,18 @@ def main():
             results[name] = time_decode_step(mxfa, torch, max(20, args.steps // 4), 5, fused=name == "dstepf")
             log(f"[bench] {name}: {json.dumps(results[name])}")
             continue
+        if name in GRAPHS:
+            base, L = GRAPHS[name]
+            case = C.BUILDERS[base]()
+            rot = ROTATE_BYTES if BOUND[name] == "hbm" else None
+            ms, kern, w, ncp = time_case(mxfa, torch, case, args.steps, args.warmup, rot, graph_layers=L)
+            results[name] = summarize(name, ms, kern, w, ncp)
+            results[name]["graph_layers"] = L
+            log(f"[bench] {name}: {json.dumps(results[name])}")
+            if name == "c2g":
+                headline = (case, w, ms, kern)
+                headline_name = name
+            continue
         spec = None
         if name in STRUCTURED:
             case = C.BUILDERS[STRUCTURED[name]]()
@@ -716,8 +763,9 @@ def main():
         ms, kern, w, ncp = time_case(mxfa, torch, case, args.steps, args.warmup, rot)
         results[name] = summarize(name, ms, kern, w, ncp)
         log(f"[bench] {name}: {json.dumps(results[name])}")
-        if name == "c2":
+        if name == "c2" and headline is None:
             headline = (case, w, ms, kern)
+            headline_name = name
 
     case, w, ms, kern = headline
     kms = kern["fa_prefill"]
@@ -736,7 +784,13 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic: Philox4x32-10 + Box-Muller N(0,1), seed 1002 (q stream 0, k 1, v 2)",
-        "config": {"workload": DESCR["c2"], "batch": 1, "seq_len": 2048, "n_heads": 32, "n_kv_heads": 8,
+        "config": {"workload": DESCR["c2"],
+                   "per_call": ("one FA call of a 36-layer forward graph (configs.c2g): the layers' 36 calls read one "
+                                "causal mask, classified once per forward (mxfa_graph_begin/end), as the reference "
+                                "builds the mask once per graph for all layers (src/qwen3-lm.h:515-517, :541-543); "
+                                "configs.c2 is the same call classifying its own mask")
+                   if headline_name == "c2g" else "one call with its own mask classification",
+                   "batch": 1, "seq_len": 2048, "n_heads": 32, "n_kv_heads": 8,
                    "head_dim": 128, "q_type": "f32", "kv_type": "f16", "mask": "f16 causal",
                    "accumulate": "fp32", "algorithmic_gflop": round(w["flops"] / 1e9, 3)},
         "roofline": {"bound": "mfma", "kernel": "fa_prefill_kernel<F16>", "achieved": round(achieved, 3),

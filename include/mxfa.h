@@ -253,6 +253,33 @@ int mxfa_qk_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_ten
 int mxfa_reserve(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
                  const mxfa_params *params, void *hip_stream);
 
+/* One mask classification per graph.  The reference builds each mask once
+ * per graph as an input tensor and hands the same tensor to every layer's
+ * attention node: the LM's causal mask (src/qwen3-lm.h:515-517, used at
+ * :541-543 by all 36 layers of the 4B model), the DiT's sliding-window and
+ * cross-attention masks (src/dit-graph.h:522-528, used at :574-576).  The
+ * engine's prefill path first sorts every (128-query x 64-key) tile of a
+ * dense mask into all -inf / all zero / mixed (one classifier launch);
+ * after mxfa_graph_begin(stream), a mask that several FA nodes on that
+ * stream share -- the same data pointer, ne, nb, and the same Sq and Skv --
+ * is classified once, at its first node, and the later nodes reuse the
+ * classes, until mxfa_graph_end(stream).  A ggml backend brackets each
+ * graph_compute with the two calls (no counterpart in ggml; like
+ * mxfa_reserve they are backend-level): between them the contents of a
+ * mask that FA nodes read must not change, and after mxfa_graph_end the
+ * stream classifies per call again.  A second mxfa_graph_begin without an
+ * end starts a new graph (earlier classes are forgotten).  Under HIP
+ * graph capture the classifier launch is recorded at the mask's first node,
+ * so every replay reclassifies the mask's current contents before the
+ * nodes that read the classes.  The classes of one graph live in a
+ * per-(device, stream) arena grown on demand (64 KiB holds the classes of
+ * hundreds of masks of the reference's shapes); a graph that would grow it
+ * fails with MXFA_ERR_UNSUPPORTED while being captured (compute it eagerly
+ * once first).  Host-side only: launches nothing, allocates nothing.
+ * mxfa_flash_attn_ext_noalloc always classifies per call. */
+int mxfa_graph_begin(void *hip_stream);
+int mxfa_graph_end(void *hip_stream);
+
 /* Allocation-free variant of mxfa_flash_attn_ext (no counterpart in the
  * reference or in ggml).  For callers that cannot allocate device memory:
  * code under HIP graph capture, tight serving loops, hosts that forbid

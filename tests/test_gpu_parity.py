@@ -13,7 +13,10 @@ same bytes with three references:
   strict ggml's CPU kernel as it runs (fp16 running accumulator for F16 V).
          Its own distance to exact maths exceeds the bar on long F16 rows,
          so it is asserted through the triangle: the GPU may be no further
-         from strict ggml than exact maths is, plus 1e-3 / 1e-5 in cosine.
+         from strict ggml than exact maths is, plus the GPU's own distance
+         from exact maths and 1e-4 in max-abs (1e-6 in cosine), never more
+         than 1e-3 (1e-5) in all (the full-size configs sit within 5e-5 /
+         1e-7 of strict's own distance).
 """
 from __future__ import annotations
 
@@ -86,8 +89,11 @@ def check(mx, case, label, exact=True, strict=True, n_threads=None):
         assert res["exact"]["max_abs"] <= tol and res["exact"]["min_cos"] >= ROW_COS_TOL, (label, res["exact"])
     if strict and exact:
         sv = res["strict_vs_exact"]
-        assert res["strict"]["max_abs"] <= sv["max_abs"] + 1e-3, (label, res)
-        assert res["strict"]["min_cos"] >= sv["min_cos"] - 1e-5, (label, res)
+        ge = res["exact"]
+        slack_abs = min(1e-3, 1e-4 + ge["max_abs"])
+        slack_cos = min(1e-5, 1e-6 + (1.0 - ge["min_cos"]))
+        assert res["strict"]["max_abs"] <= sv["max_abs"] + slack_abs, (label, res)
+        assert res["strict"]["min_cos"] >= sv["min_cos"] - slack_cos, (label, res)
     return got, res
 
 
@@ -142,6 +148,26 @@ def test_c4_dit_self_bf16(mx):
     check(mx, cases.c4_self(kv_type=cases.TYPE_BF16, Nkv=8), "C4 self 3000 bf16 16/8 (gate)",
           exact=False, strict=False)
     check(mx, cases.c4_self(kv_type=cases.TYPE_BF16, S=1024), "C4 self 1024 bf16")
+
+
+@pytest.mark.parametrize("nkv", [16, 8])
+def test_c4_dit_window_layer(mx, nkv):
+    """The DiT's sliding-window self-attention layer (every even layer,
+    dit-graph.h:574-576) at full size: the dense F16 window mask
+    [3000, 3000, 1, 2] the reference uploads (dit-sampler.h:262-289), window
+    128, against gate, exact and strict; then the same layer with the
+    window as metadata, bitwise equal to the dense call."""
+    import torch
+
+    from mxfa import cases
+
+    c = cases.c4_self_window() if nkv == 16 else cases.c4_self_window8()
+    got, _ = check(mx, c, f"C4 window 128, 16/{nkv}")
+    dq, dk, dv = mx.upload(c.q), mx.upload(c.k), mx.upload(c.v)
+    out = mx.flash_attn_ext_masked(dq, dk, dv, mx.mask_spec(**cases.structured_spec(c)), c.scale)
+    torch.cuda.synchronize()
+    got_sm = mx.output_tensor(out).cpu().numpy()
+    assert np.array_equal(got_sm, got), f"structured window differs from dense: max {np.abs(got_sm - got).max()}"
 
 
 def test_c4_dit_cross(mx):
