@@ -56,6 +56,7 @@
 
 #include "mxfa_common.h"
 #include "mxfa_internal.h"
+#include "once_per_device.h"
 
 namespace mxfa {
 
@@ -1190,13 +1191,17 @@ constexpr int kDecStages = 2;   // LDS ring depth of fa_decode_lds_kernel (2 wor
 template <int KT, int MM>
 static hipError_t launch_lds(const FaArgs &a, dim3 grid, hipStream_t stream) {
     constexpr int bytes = lds_bytes_lds_kernel<kDecStages>();
-    static bool attr_set = false;   // a per-function attribute
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute((const void *)fa_decode_lds_kernel<KT, MM, kDecStages>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    // the dynamic LDS limit is a per-(function, device) attribute: set once
+    // on each device that launches this instance
+    static OncePerDevice attr;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    e = attr.run(dev, [] {
+        return hipFuncSetAttribute((const void *)fa_decode_lds_kernel<KT, MM, kDecStages>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    });
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((fa_decode_lds_kernel<KT, MM, kDecStages>), grid, dim3(256), bytes, stream, a);
     return hipGetLastError();
 }

@@ -388,8 +388,12 @@ int check_spec(const mxfa_mask_spec *sm, const mxfa_tensor *q) {
     return MXFA_OK;
 }
 
+// ws_cap: workspace bytes the call may use (the allocation-free entry
+// point's fixed scratch); a prompt over a Q8_0 cache whose F16 staging does
+// not fit takes the decode kernel instead, which stages nothing.
 void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const mxfa_tensor *mask,
-               const mxfa_params *p, mxfa_tensor *dst, Plan &pl, const mxfa_mask_spec *sm = nullptr) {
+               const mxfa_params *p, mxfa_tensor *dst, Plan &pl, const mxfa_mask_spec *sm = nullptr,
+               size_t ws_cap = SIZE_MAX) {
     FaArgs &a = pl.args;
     const bool sm_dev = sm && (sm->flags & MXFA_MASK_DEVICE);
     if (sm && (sm->flags & ~MXFA_MASK_DEVICE)) {
@@ -474,8 +478,13 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     const bool offsets_32 = (uint64_t)n_kt * kPfBN * row_bytes <= 0xFFFFFFFFull;
     const int64_t n_kv_rows = k->ne[1] * k->ne[2] * k->ne[3];
     const bool stage_ok = !q8 || 32 * n_kv_rows < ((int64_t)1 << 31);
+    // (classes of every mask plane, then 256 B of F16 staging per K and per
+    // V row; bounds as in the prefill branch below)
+    const uint64_t n_qt_pf = (uint64_t)(a.Sq + kPfBM - 1) / kPfBM, n_kt_pad_pf = ((uint64_t)n_kt + 3) & ~3ull;
+    const uint64_t cls_pf = mask ? (uint64_t)a.m_ne2 * a.m_ne3 * n_qt_pf * n_kt_pad_pf : 0;
+    const bool stage_fits = !q8 || ((cls_pf + 255) & ~255ull) + 512ull * (uint64_t)n_kv_rows <= ws_cap;
     pl.prefill = (k->type == MXFA_TYPE_F16 || k->type == MXFA_TYPE_BF16 || q8) && a.Sq >= kPrefillMinSq &&
-                 mask_vec_ok && offsets_32 && stage_ok && (!mask || n_kt <= kPfMaxKeyTiles);
+                 mask_vec_ok && offsets_32 && stage_ok && stage_fits && (!mask || n_kt <= kPfMaxKeyTiles);
     if (pl.prefill) {
         a.n_qt = (a.Sq + kPfBM - 1) / kPfBM;
         a.n_kt = (int32_t)n_kt;
@@ -656,7 +665,10 @@ int ensure_workspace(size_t bytes, int64_t n_tickets, hipStream_t stream, void *
     // An outgrown buffer is retired, not freed: kernels queued on the
     // stream, and graphs captured earlier, keep using its address.
     if (ws.size < bytes) {
-        size_t want = bytes + bytes / 4;
+        // at least double: a prompt continued over a growing cache (Q8_0
+        // staging grows with Skv) regrows O(log) times, and the retired
+        // chain stays below the final size
+        size_t want = std::max(bytes + bytes / 4, 2 * ws.size);
         want = (want + 4095) & ~(size_t)4095;
         void *p = nullptr;
         e = hipMalloc(&p, want);
@@ -783,7 +795,7 @@ int run(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const 
         const Scratch *fixed = nullptr) {
     hipStream_t stream = (hipStream_t)hip_stream;
     Plan pl;
-    make_plan(q, k, v, mask, params, dst, pl, sm);
+    make_plan(q, k, v, mask, params, dst, pl, sm, fixed ? fixed->ws_bytes : SIZE_MAX);
     void *ws = nullptr;
     if (!pl.prefill && (int64_t)pl.args.Nkv * pl.args.row_tiles > 65535)
         return fail(MXFA_ERR_UNSUPPORTED, "too many query rows per KV head for the decode kernel");

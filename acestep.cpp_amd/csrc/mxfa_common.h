@@ -128,7 +128,7 @@ __host__ __device__ __forceinline__ void sm_row_range(const FaArgs &a, int b, in
 #if defined(__HIP_DEVICE_COMPILE__)
     if (a.sm_pos0_dev) {
         const int d = sm_dev_load(a.sm_pos0_dev);
-        p0 = d < 0 ? 0 : (d > (1 << 30) ? (1 << 30) : d);
+        p0 = d < 0 ? 0 : (d > (1 << 30) - 1 ? (1 << 30) - 1 : d);
     }
 #endif
     const int p = p0 + iq1;

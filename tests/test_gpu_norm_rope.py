@@ -372,11 +372,13 @@ def test_pipeline_batched_decode(mx):
 
 
 @pytest.mark.parametrize("out_type", [1, 30])
-def test_cross_attention_chain(mx, out_type):
+@pytest.mark.parametrize("S,E", [(300, 77), (64, 300)])
+def test_cross_attention_chain(mx, out_type, S, E):
     """DiT cross-attention's pre-attention step (src/dit-graph.h:317-346):
-    QK-norm on S = 300 queries and on enc_S = 77 encoder keys, no RoPE
-    (positions = NULL), V cast; Q out [128, Nh, S, B], K/V [128, enc_S, Nkv,
-    B].  The kernel's rows against the oracle's (ora_qk_norm) cast to 16
+    QK-norm on S queries and on enc_S = E encoder keys (fewer keys than
+    queries, and more: the kernel's grid follows the larger count and
+    switches off the rows of the other), no RoPE (positions = NULL), V cast;
+    Q out [128, Nh, S, B], K/V [128, enc_S, Nkv, B].  The kernel's rows against the oracle's (ora_qk_norm) cast to 16
     bits, V bit-exact; then attention on its 16-bit Q with the encoder
     padding mask against the oracle's F32 chain at the attention bar."""
     import torch
@@ -384,8 +386,8 @@ def test_cross_attention_chain(mx, out_type):
     import oracle
     from mxfa import cases as C
 
-    B, S, E, Nh, Nkv = 2, 300, 77, 16, 8
-    rng = np.random.default_rng(4242 + out_type)
+    B, Nh, Nkv = 2, 16, 8
+    rng = np.random.default_rng(4242 + out_type + S)
     xq = (rng.standard_normal((B, S, Nh, D)) * 3).astype(np.float32)      # projection [D, Nh, S, B]
     xkv = (rng.standard_normal((B, E, 2 * Nkv, D)) * 3).astype(np.float32)  # fused K|V [D, 2 Nkv, E, B]
     qw = (1.0 + 0.3 * rng.standard_normal(D)).astype(np.float32)
@@ -444,3 +446,58 @@ def test_cross_attention_chain(mx, out_type):
     m = row_metrics(got, ref)
     print(f"[cross] chain type={out_type}: max_abs={m['max_abs']:.3e} min_cos={m['min_cos']:.7f}", flush=True)
     assert m["max_abs"] <= MAX_ABS_TOL and m["min_cos"] >= ROW_COS_TOL, m
+
+
+def test_cross_chain_rows_more_keys_than_queries(mx):
+    """The cross form with enc_S = 300 > S = 64 and explicit cache rows:
+    encoder token e of batch b goes to row rows[e, b % 2] of a 400-row K/V
+    view; rows no token names keep their bytes."""
+    import torch
+
+    import oracle
+
+    B, S, E, Nh, Nkv, M = 2, 64, 300, 8, 4, 400
+    rng = np.random.default_rng(977)
+    xq = (rng.standard_normal((B, S, Nh, D)) * 3).astype(np.float32)
+    xkv = (rng.standard_normal((B, E, 2 * Nkv, D)) * 3).astype(np.float32)
+    qw = (1.0 + 0.3 * rng.standard_normal(D)).astype(np.float32)
+    kw = (1.0 + 0.3 * rng.standard_normal(D)).astype(np.float32)
+    rows = np.stack([rng.permutation(M)[:E] for _ in range(2)], axis=1).astype(np.int64)   # [E, 2]
+    dq, dkv = torch.from_numpy(xq).cuda(), torch.from_numpy(xkv).cuda()
+    dqw, dkw = torch.from_numpy(qw).cuda(), torch.from_numpy(kw).cuda()
+    drows = torch.from_numpy(np.ascontiguousarray(rows.T)).cuda()   # memory [2][E]: ne = (E, 2)
+    qo = torch.zeros((B, S, Nh, D), dtype=torch.int16, device="cuda")
+    sentinel = 0x1234
+    ko = torch.full((B, Nkv, M, D), sentinel, dtype=torch.int16, device="cuda")
+    vo = torch.full_like(ko, sentinel)
+    V = mx.DeviceView
+    kvnb = (4, 4 * D, 4 * D * 2 * Nkv, 4 * D * 2 * Nkv * E)
+    wnb = (4, 4 * D, 4 * D, 4 * D)
+    onb = (2, 2 * D, 2 * D * M, 2 * D * M * Nkv)
+    print(f"[cross] rows: S={S} enc_S={E} M={M}", flush=True)
+    mx.qk_norm_rope(V(0, (D, Nh, S, B), (4, 4 * D, 4 * D * Nh, 4 * D * Nh * S), dq.data_ptr(), dq),
+                    V(0, (D, Nkv, E, B), kvnb, dkv.data_ptr(), dkv),
+                    V(0, (D, Nkv, E, B), kvnb, dkv.data_ptr() + 4 * D * Nkv, dkv),
+                    V(0, (D, 1, 1, 1), wnb, dqw.data_ptr(), dqw), V(0, (D, 1, 1, 1), wnb, dkw.data_ptr(), dkw),
+                    None, EPS, BASE,
+                    V(1, (D, Nh, S, B), (2, 2 * D, 2 * D * Nh, 2 * D * Nh * S), qo.data_ptr(), qo),
+                    V(1, (D, M, Nkv, B), onb, ko.data_ptr(), ko), V(1, (D, M, Nkv, B), onb, vo.data_ptr(), vo),
+                    V(27, (E, 2, 1, 1), (8, 8 * E, 16 * E, 16 * E), drows.data_ptr(), drows))
+    torch.cuda.synchronize()
+    rq = oracle.qk_norm(xq, qw, EPS)
+    rk = oracle.qk_norm(xkv[:, :, :Nkv], kw, EPS)      # [B, E, Nkv, D]
+    rv = xkv[:, :, Nkv:]
+    g = qo.cpu().numpy().view(np.uint16)
+    r16 = _to16(np.ascontiguousarray(rq), 1)
+    assert np.all(np.abs(_from16(g, 1).astype(np.float64) - _from16(r16, 1)) <= _ulp16(_from16(r16, 1), 1))
+    kh, vh = ko.cpu().numpy().view(np.uint16), vo.cpu().numpy().view(np.uint16)
+    named = np.zeros((B, M), dtype=bool)
+    for b in range(B):
+        for e in range(E):
+            r = rows[e, b % 2]
+            named[b, r] = True
+            gk, rk16 = kh[b, :, r], _to16(np.ascontiguousarray(rk[b, e]), 1)
+            assert np.all(np.abs(_from16(gk, 1).astype(np.float64) - _from16(rk16, 1)) <= _ulp16(_from16(rk16, 1), 1)), (b, e)
+            assert np.array_equal(vh[b, :, r], _to16(np.ascontiguousarray(rv[b, e]), 1)), (b, e)
+    for b in range(B):
+        assert np.all(kh[b][:, ~named[b]] == sentinel) and np.all(vh[b][:, ~named[b]] == sentinel), b

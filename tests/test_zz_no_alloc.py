@@ -64,8 +64,9 @@ def test_noalloc_prefill_matches_workspace_entry(mx):
 
 
 def test_noalloc_q8_0_prefill_matches_workspace_entry(mx):
-    """Prefill over a Q8_0 cache (tile classes and the F16 staging of Q, K
-    and V in the scratch): two calls, the second smaller."""
+    """Prefill over a Q8_0 cache (tile classes and the F16 staging of K and
+    V in the scratch; Q is quantised to Q8_0 on load): two calls, the second
+    smaller."""
     from test_gpu_parity import _rand_case
 
     for label, case in (("q8-300", _rand_case(811, B=2, Sq=300, Nh=8, Nkv=2, Skv=516, kv_type=8, mask="causal")),
@@ -73,6 +74,34 @@ def test_noalloc_q8_0_prefill_matches_workspace_entry(mx):
         print(f"[noalloc] q8_0 prefill {label}: q{tuple(case.q.ne)} k{tuple(case.k.ne)}", flush=True)
         got, ref = _both(mx, case)
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (label, float(np.abs(got - ref).max()))
+
+
+def test_noalloc_q8_0_prompt_larger_than_the_staging(mx):
+    """C2's prompt over a Q8_0 cache (16384 K/V rows: 8 MiB of F16 staging,
+    more than the scratch holds) runs through the decode kernel, which
+    stages nothing, at the parity bar against the oracle; then a small
+    Q8_0 prompt, whose staging fits, takes the prefill kernel again and
+    equals the workspace entry point bit for bit."""
+    import oracle
+    import torch
+
+    from conftest import MAX_ABS_TOL, ROW_COS_TOL, row_metrics
+    from mxfa import cases as C
+    from test_gpu_parity import _rand_case
+
+    case = C.c2_q8()
+    print(f"[noalloc] c2q8: q{tuple(case.q.ne)} k{tuple(case.k.ne)}", flush=True)
+    dq, dk, dv, dm = mx.upload(case.q), mx.upload(case.k), mx.upload(case.v), mx.upload(case.mask)
+    out = mx.flash_attn_ext_noalloc(dq, dk, dv, dm, case.scale)
+    torch.cuda.synchronize()
+    got = mx.output_tensor(out).cpu().numpy()
+    gate = oracle.fa_ggml(case.q, case.k, case.v, case.mask, case.scale, acc_f32=True)
+    m = row_metrics(got, gate)
+    print(f"[noalloc] c2q8 vs gate: max_abs={m['max_abs']:.3e} min_cos={m['min_cos']:.7f}", flush=True)
+    assert m["max_abs"] <= MAX_ABS_TOL and m["min_cos"] >= ROW_COS_TOL, m
+    small = _rand_case(813, B=1, Sq=128, Nh=8, Nkv=2, Skv=300, kv_type=8, mask="causal")
+    got, ref = _both(mx, small)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), float(np.abs(got - ref).max())
 
 
 def test_noalloc_allocates_nothing_in_the_engine(mx):
