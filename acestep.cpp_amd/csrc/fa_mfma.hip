@@ -60,6 +60,7 @@ constexpr uint32_t kCusPerXcd = 32;          // 256 CUs
 #define MXFA_PF_LOOK 2
 #endif
 constexpr int kPfLook = MXFA_PF_LOOK;        // LDS operand reads ahead of their MFMA (1..7)
+constexpr int kPfEarlyMaxKt = 4;             // key tiles up to which a tile's copies go out before it
 static_assert(kPfLook >= 1 && kPfLook <= 7, "operand ring holds 8");
 
 __global__ void __launch_bounds__(256) mask_classify_kernel(const FaArgs a, uint8_t *cls) {
@@ -160,7 +161,10 @@ __device__ __forceinline__ float sum_pair32(float x) {
 // arithmetic on (query row, key) -- no classifier pass, no mask reads.
 // QQ8: Q quantised to Q8_0 on load, as ggml quantises Q for a Q8_0 K (the
 // K/V rows of a Q8_0 cache are staged in F16 by q8_stage.hip first).
-template <int T, bool CAP, bool SM, bool QQ8>
+// SPREAD: the next tile's copies go out one per QK MFMA of the current
+// tile (true), or all before the tile (false: calls of at most
+// kPfEarlyMaxKt key tiles).
+template <int T, bool CAP, bool SM, bool QQ8, bool SPREAD = true>
 __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
     using MF = Mfma32<T>;
     using V8 = typename MF::v8;
@@ -494,12 +498,12 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
     // that consumes them (a ring of 8 operand registers).
     //
     // kn is the next live tile (n_kt: none), whose copies into the other
-    // stage NST go out one per QK MFMA of half a: spread so, their issue
-    // (~40 cycles each, with the LDS address set per copy) hides under the
-    // matrix cores instead of holding up the tile's first MFMAs.
+    // stage NST go out one per QK MFMA of half a (SPREAD): spread so, their
+    // issue (~40 cycles each, with the LDS address set per copy) hides under
+    // the matrix cores instead of holding up the tile's first MFMAs.
     auto tile = [&](auto st_c, int kt, auto nst_c, int kn) __attribute__((always_inline)) {
         constexpr int NST = decltype(nst_c)::value;
-        const bool do_issue = kn < n_kt;   // uniform
+        const bool do_issue = SPREAD && kn < n_kt;   // uniform
         const uint32_t nl0 = lds0 + NST * kStageBytes + (uint32_t)(16 * wave) * 256u;
         i32x4 nrk = {0, 0, 0, 0}, nrv = {0, 0, 0, 0};
         if (do_issue) {
@@ -607,23 +611,26 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
     // wave's copies of the tile, one barrier (every wave's copies have
     // landed and every wave is done with the other stage), compute, with the
     // next live tile's copies into the other stage spread over the first
-    // MFMAs.  Measured against issuing them all before the tile: C2 52.5
-    // against 53.8 us, C4 self 157 against 160, and C4 cross (4 tiles per
-    // job, bound by memory latency) 35.3 against 34.6.  (No divergent early
-    // exits anywhere: they would put the tile loop under divergent control
-    // flow.)
+    // MFMAs (SPREAD) or issued before them.  Measured, spread against
+    // before: C2 52.5 against 53.8 us, C4 self 157 against 160, and C4
+    // cross (4 tiles per job, bound by memory latency) 35.3 against 34.6,
+    // so calls of few key tiles take the other instance.  (No divergent
+    // early exits anywhere: they would put the tile loop under divergent
+    // control flow.)
     std::integral_constant<int, 0> st0;
     std::integral_constant<int, 1> st1;
     while (kt < n_kt) {
         int kn = next_live(kt + 1);
         MXFA_WAIT_VMCNT(0);
         __builtin_amdgcn_s_barrier();
+        if (!SPREAD && kn < n_kt) issue(kn, st1);
         tile(st0, kt, st1, kn);
         kt = kn;
         if (kt >= n_kt) break;
         kn = next_live(kt + 1);
         MXFA_WAIT_VMCNT(0);
         __builtin_amdgcn_s_barrier();
+        if (!SPREAD && kn < n_kt) issue(kn, st0);
         tile(st1, kt, st0, kn);
         kt = kn;
     }
@@ -643,10 +650,10 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
     }
 }
 
-template <int T, bool CAP, bool SM>
+template <int T, bool CAP, bool SM, bool SPREAD>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fa_prefill_kernel(const FaArgs a) {
-    fa_prefill_body<T, CAP, SM, false>(a);
+    fa_prefill_body<T, CAP, SM, false, SPREAD>(a);
 }
 
 // Prefill over a Q8_0 cache: K/V rows staged in F16, Q quantised on load.
@@ -665,7 +672,12 @@ hipError_t launch_mask_classify(const FaArgs &a, int n_planes, uint8_t *classes,
 hipError_t launch_fa_prefill(const FaArgs &a, int ktype, hipStream_t stream) {
     dim3 grid((uint32_t)a.n_qt * (uint32_t)a.Nh * (uint32_t)a.B);
     const bool cap = a.softcap != 0.0f, sm = a.sm_flags != 0;
-#define MXFA_PF(TT, C, S) hipLaunchKernelGGL((fa_prefill_kernel<TT, C, S>), grid, dim3(256), kPfLds, stream, a)
+    const bool spread = a.n_kt > kPfEarlyMaxKt;
+#define MXFA_PF(TT, C, S)                                                                                    \
+    do {                                                                                                     \
+        if (spread) hipLaunchKernelGGL((fa_prefill_kernel<TT, C, S, true>), grid, dim3(256), kPfLds, stream, a); \
+        else hipLaunchKernelGGL((fa_prefill_kernel<TT, C, S, false>), grid, dim3(256), kPfLds, stream, a);       \
+    } while (0)
     if (ktype == T_F16) {
         if (sm) { if (cap) MXFA_PF(T_F16, true, true); else MXFA_PF(T_F16, false, true); }
         else { if (cap) MXFA_PF(T_F16, true, false); else MXFA_PF(T_F16, false, false); }
