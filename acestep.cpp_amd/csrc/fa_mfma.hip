@@ -320,7 +320,50 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
     // rounded to T (round to nearest even, as ggml converts Q to K's
     // vec-dot type), or already stored in T (a.q16).
     V8 qb[8];
-    {
+    if constexpr (!SPREAD && !QQ8) {
+        // Calls of few key tiles are bound by their Q and O bytes: Q comes
+        // in as whole rows (2 F32 rows or 4 16-bit rows per 16-byte load,
+        // whole 128-byte lines), goes through the wave's 8 KB of the free
+        // stage (16-byte chunk k of a row at slot k ^ (row & 15)) and is
+        // read back in the operand layout.  Rows past Sq load the last row;
+        // their outputs are not stored.
+        const char *qhead = a.q + (int64_t)head * a.q_nb2 + (int64_t)b * a.q_nb3;
+        const int q0w = qt * kPfBM + wave * 32;
+        uint8_t *qst = smem + kStageBytes + wave * 8192;
+        if (a.q16) {
+            u16x8 xr[8];   // load i: rows 4i + lane/16, chunk lane%16
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int row = min(q0w + 4 * i + (lane >> 4), a.Sq - 1);
+                xr[i] = *(const u16x8 *)(qhead + (int64_t)row * a.q_nb1 + 16 * (lane & 15));
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int rl = 4 * i + (lane >> 4);
+                *(u16x8 *)(qst + rl * 256 + 16 * ((lane & 15) ^ (rl & 15))) = xr[i];
+            }
+        } else {
+            f32x4 xq[16];  // load i: rows 2i + lane/32, dims 4(lane%32) .. +3
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int row = min(q0w + 2 * i + (lane >> 5), a.Sq - 1);
+                xq[i] = *(const f32x4 *)(qhead + (int64_t)row * a.q_nb1 + 16 * (lane & 31));
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int rl = 2 * i + (lane >> 5), c4 = lane & 31;
+                const u16x8 hv = cvt8<T>(xq[i], xq[i]);
+                *(u16x4 *)(qst + rl * 256 + 16 * ((c4 >> 1) ^ (rl & 15)) + 8 * (c4 & 1)) =
+                    u16x4{hv[0], hv[1], hv[2], hv[3]};
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+            qb[t] = __builtin_bit_cast(V8, *(const u16x8 *)(qst + l32 * 256 + 16 * ((2 * t + h) ^ (l32 & 15))));
+        // (every wave's staging reads are done before the first tile's
+        // barrier, after which the stage takes the next tile's copies)
+        MXFA_WAIT_LGKMCNT0();
+    } else {
         const char *qrow_p = a.q + (int64_t)qrow_c * a.q_nb1 + (int64_t)head * a.q_nb2 + (int64_t)b * a.q_nb3;
         if (a.q16) {
             const uint16_t *qh = (const uint16_t *)qrow_p;
