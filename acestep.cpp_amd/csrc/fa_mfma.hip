@@ -45,17 +45,11 @@
 
 #include <type_traits>
 
-#include "mxfa_common.h"
-#include "mxfa_internal.h"
+#include "fa_prefill.h"
 
 
 namespace mxfa {
 
-constexpr int kTileBytes = 16384;            // K or V rows of one 64-key tile
-constexpr int kStageBytes = 2 * kTileBytes;  // K + V
-constexpr int kPfLds = 2 * kStageBytes;      // double buffered: 64 KB
-constexpr uint32_t kXcds = 8;                // MI355X: workgroups go round-robin to 8 XCDs
-constexpr uint32_t kCusPerXcd = 32;          // 256 CUs
 #ifndef MXFA_PF_LOOK
 #define MXFA_PF_LOOK 2
 #endif
@@ -122,40 +116,6 @@ __global__ void __launch_bounds__(256) mask_classify_kernel(const FaArgs a, uint
     }
 }
 
-// Tile classes of one (plane, query tile) row live in registers: lane l
-// holds the class bytes of key tiles 4l..4l+3 (w0: tiles < 256, w1: tiles
-// 256..511), read with v_readlane (uniform, no memory wait in the loop).
-struct TileClasses {
-    uint32_t w0, w1;
-    bool present;
-    __device__ __forceinline__ int at(int kt) const {
-        if (!present) return 1;
-        const uint32_t w = kt < 256 ? __builtin_amdgcn_readlane(w0, (kt >> 2) & 63)
-                                    : __builtin_amdgcn_readlane(w1, ((kt - 256) >> 2) & 63);
-        return (int)((w >> (8 * (kt & 3))) & 0xFFu);
-    }
-    // (readfirstlane: the result is wave-uniform, and the compiler must
-    // know it to keep the tile loop on scalar branches)
-    __device__ __forceinline__ int next_live(int kt, int n) const {
-        if (!present) return kt;
-        while (kt < n && at(kt) == 0) kt++;
-        return __builtin_amdgcn_readfirstlane(kt);
-    }
-};
-
-// Max of a lane's value and the same register of lane l ^ 32 (one
-// v_permlane32_swap: lanes l and l ^ 32 hold the two key halves of a query).
-__device__ __forceinline__ float max_pair32(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
-                                                    false, false);
-    return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
-}
-__device__ __forceinline__ float sum_pair32(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
-                                                    false, false);
-    return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
-}
-
 // CAP: logit softcap on (a per-call constant; its tanh path is compiled only
 // into the instances that need it, so it costs the common path no registers).
 // SM: structured mask (a.sm_*): tile classes and per-element liveness are
@@ -184,25 +144,7 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
     // that share K/V rows run on one XCD and share its L2.
     int qt, head, b;
     bool second = false;   // the CU's second workgroup of the first pair
-    {
-        const uint32_t L = __builtin_amdgcn_workgroup_id_x();
-        const uint32_t N = (uint32_t)(a.n_qt * a.Nh * a.B);
-        const uint32_t nq = N / kXcds, nr = N % kXcds, x = L % kXcds, s0 = L / kXcds;
-        // Snake order over rounds of kCusPerXcd: the XCD's dispatcher gives
-        // each CU one workgroup per round, so odd rounds run reversed and a
-        // CU pairs a long causal tile with a short one.
-        const uint32_t n_x = x < nr ? nq + 1 : nq;
-        const uint32_t rnd = s0 / kCusPerXcd, w = s0 % kCusPerXcd;
-        const uint32_t cnt = min(kCusPerXcd, n_x - rnd * kCusPerXcd);
-        const uint32_t s = (rnd & 1) ? rnd * kCusPerXcd + (cnt - 1 - w) : s0;
-        const uint32_t J = x < nr ? x * (nq + 1) + s : nr * (nq + 1) + (x - nr) * nq + s;
-        const uint32_t per_u = (uint32_t)(a.G * a.n_qt);
-        const uint32_t u = J / per_u, r = J % per_u;
-        qt = __builtin_amdgcn_readfirstlane(a.n_qt - 1 - (int)(r / (uint32_t)a.G));
-        b = __builtin_amdgcn_readfirstlane((int)(u / (uint32_t)a.Nkv));
-        head = __builtin_amdgcn_readfirstlane((int)(u % (uint32_t)a.Nkv) * a.G + (int)(r % (uint32_t)a.G));
-        second = rnd == 1 && n_x >= 2 * kCusPerXcd;   // (every CU of the XCD holds a pair)
-    }
+    pf_job(a, a.n_qt, qt, head, b, second);
     // The two workgroups of a CU's first pair start together, and both would
     // first fetch Q (64 KB in F32) and their first tile.  The second one
     // waits ~2 us (s_sleep 64: 64 x 64 clocks) so that the first pair's

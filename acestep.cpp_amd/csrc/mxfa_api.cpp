@@ -78,6 +78,17 @@ std::vector<Workspace> g_ws;  // one per (device, stream) that has needed one
 
 // Query-run length from which the MFMA prefill kernel is used.
 constexpr int64_t kPrefillMinSq = 64;
+// Build option MXFA_WIDE=0 keeps every prefill call on the 32-query kernel
+// (for same-box comparisons of the two).
+#ifndef MXFA_WIDE
+#define MXFA_WIDE 1
+#endif
+constexpr bool kPfWide = MXFA_WIDE != 0;
+// Masked calls take it up to this many key tiles: a causal mask over long
+// rows would make 192-query jobs the critical path (the host cannot tell a
+// dense causal mask from a window or padding mask, and a structured mask
+// follows the same rule as its dense form).
+constexpr int64_t kPfWideMaskedMaxKt = 4;
 // Workgroups the decode kernel aims for before it splits the KV range.
 constexpr int64_t kSplitTargetWgs = 512;
 constexpr int kSplitKeyQuantum = 128;  // 4 waves x 32 keys
@@ -285,6 +296,7 @@ int check_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tenso
 
 struct Plan {
     bool prefill = false;
+    bool wide = false;   // prefill on the 48-query-per-wave kernel (fa_wide.hip)
     FaArgs args{};
     int ktype = 0;
     int n_planes = 0;
@@ -489,6 +501,19 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
         a.n_qt = (a.Sq + kPfBM - 1) / kPfBM;
         a.n_kt = (int32_t)n_kt;
         a.n_kt_pad = (a.n_kt + 3) & ~3;
+        // F16 calls without a mask (the DiT's self-attention: the reference
+        // casts K/V to F16 first) or with a dense mask over few key tiles
+        // (the DiT's cross-attention) take the kernel with 48 queries per
+        // wave: 192-query workgroups, each LDS operand read once for three
+        // MFMAs.  Same-box A/B against the 32-query kernel: C4 self 149.0
+        // against 164.0 us, C4 cross 35.1-35.6 against 37.5-37.6 us.  (BF16
+        // stays on the 32-query kernel: its P hi/lo pair does not fit the
+        // wide kernel's registers without spills.)
+        // The same rule holds for a dense mask and its structured form, so
+        // that the two stay on one kernel (bit-identical outputs).
+        pl.wide = kPfWide && k->type == MXFA_TYPE_F16 && a.softcap == 0.0f &&
+                  ((!mask && a.sm_flags == 0) || n_kt <= kPfWideMaskedMaxKt);
+        a.n_qt_w = pl.wide ? (a.Sq + kPfWideBM - 1) / kPfWideBM : 0;
         pl.n_planes = mask ? a.m_ne2 * a.m_ne3 : 0;
         pl.ws_bytes = mask ? (size_t)pl.n_planes * a.n_qt * a.n_kt_pad : 0;
         a.n_splits = 1;
@@ -845,7 +870,9 @@ int run(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const 
                 if (e != hipSuccess) return fail(MXFA_ERR_HIP, "mask classify launch: %s", hipGetErrorString(e));
             }
         }
-        e = timed_launch("fa_prefill", stream, [&] { return launch_fa_prefill(a, pl.ktype, stream); });
+        e = timed_launch("fa_prefill", stream, [&] {
+            return pl.wide ? launch_fa_wide(a, pl.ktype, stream) : launch_fa_prefill(a, pl.ktype, stream);
+        });
         if (e != hipSuccess) return fail(MXFA_ERR_HIP, "prefill launch: %s", hipGetErrorString(e));
         return MXFA_OK;
     }

@@ -73,6 +73,7 @@ struct FaArgs {
     // prefill: per (mask plane, q tile, k tile) class (see fa_mfma.hip)
     const uint8_t *tile_class;
     int32_t n_qt, n_kt;                   // tiles along Sq and Skv
+    int32_t n_qt_w;                       // fa_wide.hip: 192-query tiles along Sq (0: not used)
     int32_t n_kt_pad;                     // class row stride (n_kt rounded up to 4)
     // structured mask (sm_flags == 0: none; then `mask` may hold a dense one)
     int32_t q16;                          // Q stored in K's 16-bit type (no conversion on load)

@@ -30,6 +30,12 @@ hipError_t launch_mask_classify(const FaArgs &a, int n_planes, uint8_t *classes,
 // staged in F16 by launch_q8_stage (Q, F32, quantised to Q8_0 on load).
 hipError_t launch_fa_prefill(const FaArgs &a, int ktype, hipStream_t stream);
 
+// MFMA prefill with 48 queries per wave (fa_wide.hip): kPfWideBM-query
+// workgroups over a.n_qt_w tiles; F16 K/V, no softcap, dense mask or none
+// (tile classes as for launch_fa_prefill, over kPfBM-query tiles).
+constexpr int kPfWideBM = 192;   // query rows per workgroup (4 waves x 48)
+hipError_t launch_fa_wide(const FaArgs &a, int ktype, hipStream_t stream);
+
 // F16 staging of a prefill over a Q8_0 cache (q8_stage.hip): the Q8_0 K/V
 // rows, dequantised, into contiguous [128, Skv, Nkv, Bk] F16 buffers (the
 // prefill kernel quantises Q itself: launch_fa_prefill with T_Q8_0).  K and

@@ -180,3 +180,17 @@ def test_decode_split_grids(mx, B, Sq):
     lengths[0] = 900
     spec = dict(causal=True, pos0=900 - Sq, lengths=lengths)
     check(mx, c, spec, f"decode grids B={B} Sq={Sq}", bitwise=False)
+
+
+@pytest.mark.parametrize("i,spec", list(enumerate([
+    dict(causal=True),
+    dict(window=40, pos0=60),
+    dict(causal=True, window=70, pos0=20, lengths=[200, 150, 37]),
+])))
+def test_short_kv_wide_structured(mx, i, spec):
+    """Calls of at most 4 key tiles run the kernel with 48 queries per wave
+    in both forms (dense and structured), whose tile ranges and classes are
+    taken over the same 128-query class tiles: 300 queries (a partial second
+    192-query tile) over 200 keys, GQA 4:1, rows masked out entirely."""
+    c = _rand_case(550 + i, B=3, Sq=300, Nh=8, Nkv=2, Skv=200, mask=None)
+    check(mx, c, spec, f"short K/V wide {spec}", bitwise=True)
