@@ -276,6 +276,11 @@ def _q16_cases():
         ("bf16 prefill", _rand_case(610, B=2, Sq=200, Nh=8, Nkv=2, Skv=336, kv_type=30), None),
         ("bf16 decode", _rand_case(611, B=3, Sq=2, Nh=8, Nkv=4, Skv=700, kv_type=30), None),
         ("softcap alibi", _rand_case(612, B=1, Sq=130, Nh=8, Nkv=2, Skv=300, softcap=30.0, max_bias=8.0), None),
+        # the kernel with 48 queries per wave (no mask; masks over <= 4 key tiles)
+        ("C4 self (wide)", C.c4_self(), None),
+        ("C4 cross (wide)", C.c4_cross(), None),
+        ("C4 cross structured (wide)", C.c4_cross(), "spec"),
+        ("no mask odd shape (wide)", _rand_case(613, B=2, Bk=1, Sq=385, Nh=8, Nkv=2, Skv=333, mask=None), None),
     ]
 
 

@@ -289,6 +289,21 @@ def test_contiguous_q_and_no_mask(mx):
         check(mx, c, f"no mask contiguous q Sq={Sq}")
 
 
+@pytest.mark.parametrize("Sq,Skv,B,Bk,Nh,Nkv,mask,layout", [
+    (64, 333, 1, 1, 4, 4, None, "perm"),        # one partial 192-query tile
+    (193, 1000, 2, 1, 8, 2, None, "contig"),    # a 1-row second tile, KV batch broadcast, GQA 4:1
+    (385, 257, 1, 1, 16, 4, None, "perm"),      # three tiles, an odd key count
+    (700, 200, 2, 2, 8, 8, "random", "perm"),   # 4 key tiles under a random dense mask
+    (450, 130, 3, 1, 8, 2, "random", "perm"),   # 3 key tiles, the last one partial
+])
+def test_wide_kernel_shapes(mx, Sq, Skv, B, Bk, Nh, Nkv, mask, layout):
+    """F16 calls with no mask, or a mask over at most 4 key tiles, run the
+    kernel with 48 queries per wave (192-query workgroups): partial and
+    one-row query tiles, GQA, KV batch broadcast, odd key counts."""
+    c = _rand_case(70 + Sq, B=B, Bk=Bk, Sq=Sq, Nh=Nh, Nkv=Nkv, Skv=Skv, mask=mask, q_layout=layout)
+    check(mx, c, f"wide Sq={Sq} Skv={Skv} B={B}/{Bk} {Nh}/{Nkv} mask={mask}")
+
+
 def test_softcap_and_alibi(mx):
     for Sq in (4, 100):
         c = _rand_case(50 + Sq, B=1, Sq=Sq, Nh=16, Nkv=4, Skv=129, softcap=30.0)
