@@ -551,7 +551,11 @@ __device__ void finish_tile(const FaArgs &a, const Tile &t, int ns, const f32x4 
     // coherence point has acknowledged it, so `s_waitcnt vmcnt(0)` in every
     // wave, then the barrier, put every partial at the coherence point before
     // thread 0 issues its ticket add; the workgroup that draws the last
-    // ticket issues its loads after that add has returned.  The compiler's
+    // ticket issues its loads after that add has returned.  The compiler
+    // keeps this order: the waitcnt is an asm statement with a "memory"
+    // clobber, which no memory access may cross; the merge's loads are
+    // atomic (never speculated) and sit behind the ticket's value, which
+    // reaches every wave through LDS and a barrier.  The compiler's
     // release/acquire fences at agent scope would add a whole-L2 write-back
     // (buffer_wbl2) per wave and an L2 invalidate (buffer_inv) per ticket --
     // measured: C3 44.7 -> 140 us, C5 31 -> 57 us -- to cover ordinary
