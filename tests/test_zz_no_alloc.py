@@ -63,6 +63,20 @@ def test_noalloc_prefill_matches_workspace_entry(mx):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (label, float(np.abs(got - ref).max()))
 
 
+def test_noalloc_wide_prefill_matches_workspace_entry(mx):
+    """The kernel with 48 queries per wave under a dense mask (its tile
+    classes in the scratch): C4 cross at full size, then a smaller random
+    mask over 4 key tiles."""
+    from mxfa import cases as C
+    from test_gpu_parity import _rand_case
+
+    for label, case in (("c4x", C.c4_cross()),
+                        ("wide-300", _rand_case(814, B=1, Sq=300, Nh=8, Nkv=2, Skv=200, mask="random"))):
+        print(f"[noalloc] wide prefill {label}: q{tuple(case.q.ne)} k{tuple(case.k.ne)}", flush=True)
+        got, ref = _both(mx, case)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (label, float(np.abs(got - ref).max()))
+
+
 def test_noalloc_q8_0_prefill_matches_workspace_entry(mx):
     """Prefill over a Q8_0 cache (tile classes and the F16 staging of K and
     V in the scratch; Q is quantised to Q8_0 on load): two calls, the second
