@@ -10,7 +10,7 @@
 // LDS, double-buffered, XOR-swizzled rows), but every LDS operand now feeds
 // three MFMAs instead of one:
 //
-//   S^T[16 keys x 16 q] = K . Q^T     v_mfma_f32_16x16x32_{f16,bf16}
+//   S^T[16 keys x 16 q] = K . Q^T     v_mfma_f32_16x16x32_f16
 //                                      (A = 16 K rows x 32 dims from LDS,
 //                                      one read for the 3 query blocks;
 //                                      B = Q^T in registers all along)
@@ -48,7 +48,9 @@ __device__ __forceinline__ void fa_wide_body(const FaArgs a) {
     using V8 = typename MF::v8;
     static_assert(kD == 128, "kernel is written for D = 128");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    constexpr bool kLo = T == T_BF16;   // P as a hi/lo bf16 pair (bf16_lo)
+    // (F16 only: BF16 calls stay on fa_mfma.hip, whose P hi/lo pair would
+    // not fit this kernel's registers)
+    static_assert(T == T_F16, "F16 K/V only");
 
     const int tid = (int)__builtin_amdgcn_workitem_id_x();
     const int lane = tid & 63;
@@ -316,15 +318,14 @@ __device__ __forceinline__ void fa_wide_body(const FaArgs a) {
                 }
     };
     // Probabilities of query block qb, key block kb of a half into the P^T
-    // operand (k-slots 4kb + i), and the bf16 lo parts.
-    auto probs = [&](const f32x4 (&s)[2][3], int qb, int kb, float gs, float mneg, u16x8 (&pw)[3],
-                     u16x8 (&pl)[3]) __attribute__((always_inline)) {
+    // operand (k-slots 4kb + i).
+    auto probs = [&](const f32x4 (&s)[2][3], int qb, int kb, float gs, float mneg, u16x8 (&pw)[3])
+                     __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const float p = fast_exp2(fmaf(s[kb][qb][i], gs, mneg));
             const uint16_t hbits = MF::from_f32(p);
             pw[qb][4 * kb + i] = hbits;
-            if constexpr (kLo) pl[qb][4 * kb + i] = bf16_lo(p, hbits);
         }
     };
     auto max8 = [&](const f32x4 (&s)[2][3], int qb) __attribute__((always_inline)) {
@@ -380,18 +381,14 @@ __device__ __forceinline__ void fa_wide_body(const FaArgs a) {
                 s[kb][qb] = MF::run(__builtin_bit_cast(V8, op[n % kRing]), qv[qb][t],
                                     t == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[kb][qb]);
         };
-        auto pv3 = [&](const u16x8 (&pw)[3], const u16x8 (&pl)[3], int n) __attribute__((always_inline)) {
+        auto pv3 = [&](const u16x8 (&pw)[3], int n) __attribute__((always_inline)) {
             const int db = n & 7;
 #pragma unroll
-            for (int qb = 0; qb < 3; qb++) {
+            for (int qb = 0; qb < 3; qb++)
                 o[db][qb] = MF::run(__builtin_bit_cast(V8, op[n % kRing]), __builtin_bit_cast(V8, pw[qb]), o[db][qb]);
-                if constexpr (kLo)
-                    o[db][qb] =
-                        MF::run(__builtin_bit_cast(V8, op[n % kRing]), __builtin_bit_cast(V8, pl[qb]), o[db][qb]);
-            }
         };
         f32x4 sa[2][3], sb[2][3];
-        u16x8 pa[3], pb[3], pal[3], pbl[3];
+        u16x8 pa[3], pb[3];
 
         // ---- R1: QK a (+ the next tile's copies) ----
 #pragma unroll
@@ -421,7 +418,7 @@ __device__ __forceinline__ void fa_wide_body(const FaArgs a) {
 #pragma unroll
                 for (int qb = 0; qb < 3; qb++) mxa[qb] = max8(sa, qb);
             } else if (n <= 6) {
-                probs(sa, (n - 1) >> 1, (n - 1) & 1, gs, mneg0[(n - 1) >> 1], pa, pal);
+                probs(sa, (n - 1) >> 1, (n - 1) & 1, gs, mneg0[(n - 1) >> 1], pa);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -429,13 +426,11 @@ __device__ __forceinline__ void fa_wide_body(const FaArgs a) {
 #pragma unroll
         for (int qb = 0; qb < 3; qb++) {
             la[qb] = sum8<T>(pa[qb], 0.0f);
-            if constexpr (kLo) la[qb] = sum8<T>(pal[qb], la[qb]);
         }
         // keep the speculative softmax here, overlapped with QK b (it is
         // redone on the rare path, so it would otherwise sink past R3)
         asm volatile("" ::"v"(pa[0]), "v"(pa[1]), "v"(pa[2]), "v"(la[0]), "v"(la[1]), "v"(la[2]), "v"(mxa[0]),
                      "v"(mxa[1]), "v"(mxa[2]));
-        if constexpr (kLo) asm volatile("" ::"v"(pal[0]), "v"(pal[1]), "v"(pal[2]));
         if (general) general_x(sb, key0 + 32);
         __builtin_amdgcn_sched_barrier(0);
 
@@ -468,10 +463,9 @@ __device__ __forceinline__ void fa_wide_body(const FaArgs a) {
 #pragma unroll
             for (int qb = 0; qb < 3; qb++) {
                 const float mn = (m2[qb] == -INFINITY) ? 0.0f : -m2[qb];
-                probs(sa, qb, 0, gs, mn, pa, pal);
-                probs(sa, qb, 1, gs, mn, pa, pal);
+                probs(sa, qb, 0, gs, mn, pa);
+                probs(sa, qb, 1, gs, mn, pa);
                 la[qb] = sum8<T>(pa[qb], 0.0f);
-                if constexpr (kLo) la[qb] = sum8<T>(pal[qb], la[qb]);
             }
             // (the operand ring restarts at V^T of half a)
 #pragma unroll
@@ -486,15 +480,14 @@ __device__ __forceinline__ void fa_wide_body(const FaArgs a) {
 #pragma unroll
         for (int n = 0; n < 8; n++) {
             fetch(16 + n + kLook);
-            pv3(pa, pal, 16 + n);
-            if (n < 6) probs(sb, n >> 1, n & 1, gs, mneg[n >> 1], pb, pbl);
+            pv3(pa, 16 + n);
+            if (n < 6) probs(sb, n >> 1, n & 1, gs, mneg[n >> 1], pb);
             __builtin_amdgcn_sched_barrier(0);
         }
         float lb[3];
 #pragma unroll
         for (int qb = 0; qb < 3; qb++) {
             lb[qb] = sum8<T>(pb[qb], 0.0f);
-            if constexpr (kLo) lb[qb] = sum8<T>(pbl[qb], lb[qb]);
         }
         __builtin_amdgcn_sched_barrier(0);
 
@@ -502,7 +495,7 @@ __device__ __forceinline__ void fa_wide_body(const FaArgs a) {
 #pragma unroll
         for (int n = 0; n < 8; n++) {
             fetch(24 + n + kLook);
-            pv3(pb, pbl, 24 + n);
+            pv3(pb, 24 + n);
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
