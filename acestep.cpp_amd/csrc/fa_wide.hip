@@ -125,7 +125,8 @@ __device__ __forceinline__ void fa_wide_body(const FaArgs a) {
         sm_p0 = __builtin_amdgcn_readfirstlane(sm_p0);
         int len = a.Skv;
         if (a.sm_flags & kSmLengths) {
-            len = a.sm_len_dev ? sm_dev_load(a.sm_len_dev + b % a.sm_nlen) : a.sm_len[b % a.sm_nlen];
+            len = a.sm_len[b % a.sm_nlen];
+            if (a.sm_len_dev) len = sm_dev_load(a.sm_len_dev + b % a.sm_nlen);
             len = len < 0 ? 0 : len;
         }
         sm_hi = __builtin_amdgcn_readfirstlane(min(a.Skv, len));

@@ -403,3 +403,27 @@ def test_device_pos0_prefill_equals_host_pos0(mx):
     b = mx.flash_attn_ext_masked(dq, dk, dv, mx.mask_spec(causal=True, device_pos0=p0), c.scale)
     torch.cuda.synchronize()
     assert torch.equal(mx.output_tensor(a), mx.output_tensor(b))
+
+
+def test_device_lengths_and_pos0_wide_prefill(mx):
+    """Structured calls of at most 4 key tiles run the kernel with 48 queries
+    per wave; with lengths and pos0 in device memory they equal the same
+    calls with host values, bit for bit, and follow new device values."""
+    import torch
+
+    from test_gpu_parity import _rand_case
+
+    c = _rand_case(560, B=3, Sq=300, Nh=8, Nkv=2, Skv=200, mask=None)
+    dq, dk, dv = mx.upload(c.q), mx.upload(c.k), mx.upload(c.v)
+    lens = torch.tensor([200, 150, 37], dtype=torch.int32, device="cuda")
+    p0 = torch.tensor([20], dtype=torch.int32, device="cuda")
+    for host_lens, host_p0 in (([200, 150, 37], 20), ([90, 200, 0], 5)):
+        lens.copy_(torch.tensor(host_lens, dtype=torch.int32))
+        p0.fill_(host_p0)
+        print(f"[wide device spec] lengths {host_lens} pos0 {host_p0}", flush=True)
+        a = mx.flash_attn_ext_masked(dq, dk, dv, mx.mask_spec(causal=True, window=70, pos0=host_p0,
+                                                                 lengths=host_lens), c.scale)
+        b = mx.flash_attn_ext_masked(dq, dk, dv, mx.mask_spec(causal=True, window=70, device_pos0=p0,
+                                                                 device_lengths=lens), c.scale)
+        torch.cuda.synchronize()
+        assert torch.equal(mx.output_tensor(a), mx.output_tensor(b))
