@@ -39,9 +39,10 @@
 //
 // Masks are data, not structure: a classifier pass (mask_classify_kernel)
 // labels every (128-query x 64-key) tile of the mask as all -inf (skipped:
-// no K/V traffic, no MFMA), all zero (no mask reads) or mixed (mask read per
-// element).  The causal prefill mask thus costs half the work of the dense
-// problem and no per-element mask traffic below the diagonal.
+// no K/V traffic, no MFMA), all zero (no mask reads), mixed of 0 and -inf
+// only (a 64-bit liveness word per row, loaded one tile ahead) or mixed
+// (mask read per element).  The causal prefill mask thus costs half the
+// work of the dense problem and no per-element mask traffic.
 
 #include <type_traits>
 
@@ -94,25 +95,41 @@ __global__ void __launch_bounds__(256) mask_classify_kernel(const FaArgs a, uint
         v[pass] = __builtin_bit_cast(u16x4, __builtin_amdgcn_raw_buffer_load_b64(
                                                 rs, q * (uint32_t)a.m_nb1 + 2u * kc, 0, 0));
     }
-    bool all_ninf = true, all_zero = true;
+    bool all_ninf = true, all_zero = true, all_bin = true;
+    uint32_t live = 0;   // bit 4 pass + i: key k + i of row q_lo + r0 + 16 pass is live (0 past Skv)
 #pragma unroll
     for (int pass = 0; pass < kPfBM / 16; pass++) {
         const bool row_ok = q_lo + r0 + 16 * pass < a.Sq;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const bool ok = row_ok & (k + i < a.Skv);
-            all_ninf &= !ok | (v[pass][i] == 0xFC00u);
-            all_zero &= !ok | ((v[pass][i] & 0x7FFFu) == 0);
+            const bool ninf = v[pass][i] == 0xFC00u, zero = (v[pass][i] & 0x7FFFu) == 0;
+            all_ninf &= !ok | ninf;
+            all_zero &= !ok | zero;
+            all_bin &= !ok | ninf | zero;
+            live |= (uint32_t)(k + i < a.Skv && !ninf) << (4 * pass + i);
         }
     }
     // wave votes, then one barrier across the 4 waves
     __shared__ uint32_t votes[4];
-    const uint64_t bad_ninf = __ballot(!all_ninf), bad_zero = __ballot(!all_zero);
-    if ((threadIdx.x & 63) == 0) votes[threadIdx.x >> 6] = (bad_ninf ? 1u : 0u) | (bad_zero ? 2u : 0u);
+    const uint64_t bad_ninf = __ballot(!all_ninf), bad_zero = __ballot(!all_zero), bad_bin = __ballot(!all_bin);
+    if ((threadIdx.x & 63) == 0)
+        votes[threadIdx.x >> 6] = (bad_ninf ? 1u : 0u) | (bad_zero ? 2u : 0u) | (bad_bin ? 4u : 0u);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t any = votes[0] | votes[1] | votes[2] | votes[3];
-        cls[((int64_t)plane * a.n_qt + qt) * a.n_kt_pad + kt] = !(any & 1u) ? 0 : (!(any & 2u) ? 1 : 2);
+    const uint32_t any = votes[0] | votes[1] | votes[2] | votes[3];
+    const int c = !(any & 1u) ? 0 : (!(any & 2u) ? 1 : (!(any & 4u) && a.tile_bits ? 3 : 2));
+    if (threadIdx.x == 0) cls[((int64_t)plane * a.n_qt + qt) * a.n_kt_pad + kt] = (uint8_t)c;
+    if (c == 3) {   // (uniform) the liveness words of the tile's rows
+        uint64_t *bits = a.tile_bits + (((int64_t)plane * a.n_qt + qt) * a.n_kt + kt) * kPfBM;
+#pragma unroll
+        for (int pass = 0; pass < kPfBM / 16; pass++) {
+            // the 16 lanes of a row (one DPP row) OR their 4-key nibbles
+            // into one word
+            const uint32_t nib = (live >> (4 * pass)) & 0xFu;
+            const uint32_t lo = or_rows16(c4 < 8 ? nib << (4 * c4) : 0u);
+            const uint32_t hi = or_rows16(c4 >= 8 ? nib << (4 * (c4 - 8)) : 0u);
+            if (c4 == 0) bits[r0 + 16 * pass] = ((uint64_t)hi << 32) | lo;
+        }
     }
 }
 
@@ -131,6 +148,9 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
     using V8 = typename MF::v8;
     static_assert(kD == 128, "kernel is written for D = 128");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    // dense masks' liveness words (class-3 tiles); the Q8_0 instance keeps
+    // the mask reads (the host gives Q8_0 calls no words)
+    constexpr bool kBits = !SM && !QQ8;
 
     // (work-item / group ids through the intrinsics: always inline, scalar)
     const int tid = (int)__builtin_amdgcn_workitem_id_x();
@@ -402,7 +422,7 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
     // keys 8(r/4) + 4h + r%4 of the half).  The mask is read for every
     // general tile: on a tile of class 1 it is all zero, and without a mask
     // the resource is empty (reads return zero), so no branch is needed.
-    auto general_x = [&](f32x16 &sc, int key0) __attribute__((always_inline)) {
+    auto general_x = [&](f32x16 &sc, int key0, int cl, uint32_t bits) __attribute__((always_inline)) {
         if constexpr (SM) {
             // live keys 8j + i of [lo_rel, hi_rel) (row_hi <= Skv); the
             // zero mask value keeps the arithmetic of the dense path
@@ -416,6 +436,23 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
                     if constexpr (CAP) x = (a.softcap * fast_tanh(sc[r] * sc_in)) * kLog2e + 0.0f;
                     else x = fmaf(sc[r], sl2, 0.0f);
                     sc[r] = (off >= lo_rel && off < hi_rel) ? x : -INFINITY;
+                }
+            return;
+        }
+        if (kBits && cl == 3) {
+            // a mask of 0 and -inf only: liveness from the tile's word for
+            // this row (bits of this half's keys 8j + 4h + i; 0 past Skv)
+            // and the arithmetic of a zero mask value
+            const uint32_t w = bits >> (4 * h);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 4 * j + i;
+                    float x;
+                    if constexpr (CAP) x = (a.softcap * fast_tanh(sc[r] * sc_in)) * kLog2e + 0.0f;
+                    else x = fmaf(sc[r], sl2, 0.0f);
+                    sc[r] = ((w >> (8 * j + i)) & 1u) ? x : -INFINITY;
                 }
             return;
         }
@@ -487,7 +524,7 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
     // stage NST go out one per QK MFMA of half a (SPREAD): spread so, their
     // issue (~40 cycles each, with the LDS address set per copy) hides under
     // the matrix cores instead of holding up the tile's first MFMAs.
-    auto tile = [&](auto st_c, int kt, auto nst_c, int kn) __attribute__((always_inline)) {
+    auto tile = [&](auto st_c, int kt, auto nst_c, int kn, uint64_t tbits) __attribute__((always_inline)) {
         constexpr int NST = decltype(nst_c)::value;
         const bool do_issue = SPREAD && kn < n_kt;   // uniform
         const uint32_t nl0 = lds0 + NST * kStageBytes + (uint32_t)(16 * wave) * 256u;
@@ -499,7 +536,7 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
         const int cl = __builtin_amdgcn_readfirstlane(class_of(kt));
         const int key0 = kt * kPfBN;
         const bool general =
-            __builtin_amdgcn_readfirstlane((int)(cl == 2 || key0 + kPfBN > a.Skv || !lean_ok)) != 0;
+            __builtin_amdgcn_readfirstlane((int)(cl >= 2 || key0 + kPfBN > a.Skv || !lean_ok)) != 0;
         const float g = general ? 1.0f : sl2;   // wave-uniform
         f32x16 sa, sb;
         u16x8 op[8];
@@ -524,7 +561,7 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (general) general_x(sa, key0);
+        if (general) general_x(sa, key0, cl, (uint32_t)tbits);
         __builtin_amdgcn_sched_barrier(0);
 
         // ---- R2: QK b | softmax a (speculative) ----
@@ -545,7 +582,7 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
         // redone on the rare path, so it would otherwise sink past R3)
         asm volatile("" ::"v"(pa[0]), "v"(pa[1]), "v"(la), "v"(mxa));
         if constexpr (kLo) asm volatile("" ::"v"(pal[0]), "v"(pal[1]));
-        if (general) general_x(sb, key0 + 32);
+        if (general) general_x(sb, key0 + 32, cl, (uint32_t)(tbits >> 32));
         __builtin_amdgcn_sched_barrier(0);
 
         // ---- R3: tile max, reference update (rare rescale) ----
@@ -603,15 +640,28 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
     // so calls of few key tiles take the other instance.  (No divergent
     // early exits anywhere: they would put the tile loop under divergent
     // control flow.)
+    // A class-3 tile's liveness word of this lane's row: loaded one tile
+    // ahead, right after the tile's barrier, so that it lands with the next
+    // tile's copies (the wait at that tile's top covers both).
+    const uint64_t *brow = (kBits && tc.present && a.tile_bits)
+                               ? a.tile_bits + ((int64_t)plane * a.n_qt + qt) * a.n_kt * kPfBM + wave * 32 + l32
+                               : nullptr;
+    auto load_bits = [&](int k) __attribute__((always_inline)) -> uint64_t {
+        if (!kBits || brow == nullptr || k >= n_kt || __builtin_amdgcn_readfirstlane(class_of(k)) != 3) return 0;
+        return brow[(int64_t)k * kPfBM];
+    };
     std::integral_constant<int, 0> st0;
     std::integral_constant<int, 1> st1;
     int ofree = 1;   // the stage no tile still reads at the end
+    uint64_t cbits = load_bits(kt);
     while (kt < n_kt) {
         int kn = next_live(kt + 1);
         MXFA_WAIT_VMCNT(0);
         __builtin_amdgcn_s_barrier();
         if (!SPREAD && kn < n_kt) issue(kn, st1);
-        tile(st0, kt, st1, kn);
+        uint64_t nbits = load_bits(kn);
+        tile(st0, kt, st1, kn, cbits);
+        cbits = nbits;
         ofree = 1;
         kt = kn;
         if (kt >= n_kt) break;
@@ -619,7 +669,9 @@ __device__ __forceinline__ void fa_prefill_body(const FaArgs a) {
         MXFA_WAIT_VMCNT(0);
         __builtin_amdgcn_s_barrier();
         if (!SPREAD && kn < n_kt) issue(kn, st0);
-        tile(st1, kt, st0, kn);
+        nbits = load_bits(kn);
+        tile(st1, kt, st0, kn, cbits);
+        cbits = nbits;
         ofree = 0;
         kt = kn;
     }

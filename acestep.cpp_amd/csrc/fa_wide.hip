@@ -361,7 +361,7 @@ __device__ __forceinline__ void fa_wide_body(const FaArgs a) {
         const int cl = __builtin_amdgcn_readfirstlane(class_of(kt));
         const int key0 = kt * kPfBN;
         const bool general =
-            __builtin_amdgcn_readfirstlane((int)(cl == 2 || key0 + kPfBN > a.Skv || !lean_ok)) != 0;
+            __builtin_amdgcn_readfirstlane((int)(cl >= 2 || key0 + kPfBN > a.Skv || !lean_ok)) != 0;
         const float gs = general ? 1.0f : sl2;   // wave-uniform
         // (address bases made opaque per tile, so that the addresses derived
         // from them are formed where they are used, not kept live across the

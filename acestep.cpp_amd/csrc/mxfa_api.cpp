@@ -55,6 +55,7 @@ struct ClassEntry {
     int64_t ne[4] = {0, 0, 0, 0};
     size_t nb[4] = {0, 0, 0, 0};
     int64_t Sq = 0, Skv = 0;
+    size_t bytes = 0;   // the block's layout (classes, with or without liveness words)
     uint8_t *cls = nullptr;
 };
 
@@ -296,6 +297,8 @@ int check_norm_rope(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tenso
 
 struct Plan {
     bool prefill = false;
+    size_t cls_block = 0;   // prefill under a dense mask: tile classes, then (bits_off > 0) liveness words
+    size_t bits_off = 0;
     bool wide = false;   // prefill on the 48-query-per-wave kernel (fa_wide.hip)
     FaArgs args{};
     int ktype = 0;
@@ -495,6 +498,14 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     const uint64_t n_qt_pf = (uint64_t)(a.Sq + kPfBM - 1) / kPfBM, n_kt_pad_pf = ((uint64_t)n_kt + 3) & ~3ull;
     const uint64_t cls_pf = mask ? (uint64_t)a.m_ne2 * a.m_ne3 * n_qt_pf * n_kt_pad_pf : 0;
     const bool stage_fits = !q8 || ((cls_pf + 255) & ~255ull) + 512ull * (uint64_t)n_kv_rows <= ws_cap;
+    // the liveness words of class-3 tiles (8 bytes per query row and key
+    // tile) follow the classes when the workspace can hold them; otherwise
+    // the classifier labels such tiles 2
+    const uint64_t bits_pf = mask ? (uint64_t)a.m_ne2 * a.m_ne3 * n_qt_pf * kPfBM * (uint64_t)n_kt * 8 : 0;
+    const uint64_t with_bits = ((cls_pf + 255) & ~255ull) + ((bits_pf + 255) & ~255ull);
+    // (Q8_0 calls keep reading mask values: their prefill instance has no
+    // word path)
+    const bool bits_fit = mask && !q8 && with_bits <= ws_cap;
     pl.prefill = (k->type == MXFA_TYPE_F16 || k->type == MXFA_TYPE_BF16 || q8) && a.Sq >= kPrefillMinSq &&
                  mask_vec_ok && offsets_32 && stage_ok && stage_fits && (!mask || n_kt <= kPfMaxKeyTiles);
     if (pl.prefill) {
@@ -516,6 +527,11 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
         a.n_qt_w = pl.wide ? (a.Sq + kPfWideBM - 1) / kPfWideBM : 0;
         pl.n_planes = mask ? a.m_ne2 * a.m_ne3 : 0;
         pl.ws_bytes = mask ? (size_t)pl.n_planes * a.n_qt * a.n_kt_pad : 0;
+        if (bits_fit) {
+            pl.bits_off = (pl.ws_bytes + 255) & ~(size_t)255;
+            pl.ws_bytes = (size_t)with_bits;
+        }
+        pl.cls_block = pl.ws_bytes;
         a.n_splits = 1;
         a.chunk = a.Skv;
         if (q8) {
@@ -626,7 +642,7 @@ int graph_classes(const mxfa_tensor *mask, int64_t Sq, int64_t Skv, size_t bytes
     if (rc != MXFA_OK) return rc;
     if (w->epoch == 0) return MXFA_OK;
     for (const ClassEntry &c : w->entries) {
-        bool same = c.data == mask->data && c.Sq == Sq && c.Skv == Skv;
+        bool same = c.data == mask->data && c.Sq == Sq && c.Skv == Skv && c.bytes == bytes;
         for (int i = 0; i < 4 && same; i++) same = c.ne[i] == mask->ne[i] && c.nb[i] == mask->nb[i];
         if (same) {
             *cls = c.cls;
@@ -658,6 +674,7 @@ int graph_classes(const mxfa_tensor *mask, int64_t Sq, int64_t Skv, size_t bytes
     }
     c.Sq = Sq;
     c.Skv = Skv;
+    c.bytes = bytes;
     c.cls = w->arena + w->arena_used;
     w->arena_used = (w->arena_used + bytes + 255) & ~(size_t)255;
     w->entries.push_back(c);
@@ -857,13 +874,13 @@ int run(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v, const 
             bool classify = true;
             if (!fixed) {
                 uint8_t *gc = nullptr;
-                const int rc = graph_classes(mask, a.Sq, a.Skv, (size_t)pl.n_planes * a.n_qt * a.n_kt_pad, stream,
-                                             &gc, &classify);
+                const int rc = graph_classes(mask, a.Sq, a.Skv, pl.cls_block, stream, &gc, &classify);
                 if (rc != MXFA_OK) return rc;
                 if (gc) cls = gc;
                 else classify = true;
             }
             a.tile_class = cls;
+            a.tile_bits = pl.bits_off ? (uint64_t *)(cls + pl.bits_off) : nullptr;
             if (classify) {
                 e = timed_launch("mask_classify", stream,
                                  [&] { return launch_mask_classify(a, pl.n_planes, cls, stream); });

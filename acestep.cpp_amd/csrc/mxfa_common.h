@@ -70,8 +70,11 @@ struct FaArgs {
     int32_t dec_pair;                     // > 0: paired splits, the even split of a pair streams dec_pair keys
     float *part_o, *part_ml;
     int *tickets;                         // one per (b, kv head, row tile), zero between calls
-    // prefill: per (mask plane, q tile, k tile) class (see fa_mfma.hip)
+    // prefill: per (mask plane, q tile, k tile) class (see fa_mfma.hip), and
+    // for the mixed tiles whose values are all 0 or -inf (class 3) one 64-bit
+    // liveness word per query row (NULL: no words, no class 3)
     const uint8_t *tile_class;
+    uint64_t *tile_bits;
     int32_t n_qt, n_kt;                   // tiles along Sq and Skv
     int32_t n_qt_w;                       // fa_wide.hip: 192-query tiles along Sq (0: not used)
     int32_t n_kt_pad;                     // class row stride (n_kt rounded up to 4)
@@ -97,6 +100,14 @@ __device__ __forceinline__ uint32_t and_rows16(uint32_t v) {
     v &= dpp_u32<0x4E>(v);
     v &= dpp_u32<0x141>(v);
     v &= dpp_u32<0x140>(v);
+    return v;
+}
+// OR over the 16 lanes of each row (the same DPP steps as and_rows16).
+__device__ __forceinline__ uint32_t or_rows16(uint32_t v) {
+    v |= dpp_u32<0xB1>(v);
+    v |= dpp_u32<0x4E>(v);
+    v |= dpp_u32<0x141>(v);
+    v |= dpp_u32<0x140>(v);
     return v;
 }
 // max of x over lanes l and l ^ 16 (v_permlane16_swap pairs rows r, r ^ 1)

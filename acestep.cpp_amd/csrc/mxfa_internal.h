@@ -22,7 +22,10 @@ constexpr int kPfBN = 64;    // keys per K/V tile
 
 // Mask tile classifier: writes a.tile_class[plane][qt][kt] (row stride
 // a.n_kt_pad bytes) for every (mask plane, kPfBM-query tile, kPfBN-key
-// tile): 0 = all -inf, 1 = all zero, 2 = anything else.
+// tile): 0 = all -inf, 1 = all zero, 2 = anything else, 3 = a mix of 0 and
+// -inf only (with a.tile_bits set): then the tile's liveness goes to
+// a.tile_bits[((plane * n_qt + qt) * n_kt + kt) * kPfBM + row], bit k for key
+// k of the tile (keys past Skv: 0).
 constexpr int kPfMaxKeyTiles = 512;   // class rows held in two registers per lane
 hipError_t launch_mask_classify(const FaArgs &a, int n_planes, uint8_t *classes, hipStream_t stream);
 
