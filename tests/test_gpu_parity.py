@@ -23,6 +23,7 @@ from __future__ import annotations
 import math
 import os
 import sys
+from dataclasses import replace
 
 import numpy as np
 import pytest
@@ -436,6 +437,49 @@ def test_short_kv_many_query_tiles(mx, kind):
     else:
         c = _rand_case(303, B=4, Bk=1, Sq=600, Nh=32, Nkv=2, Skv=129, mask=None)
     check(mx, c, f"short K/V ({kind})")
+
+
+def _binary_mask(case, seed, neg_zero=0.5):
+    """The case's mask reduced to 0 and -inf in place: its -inf entries stay,
+    every other entry becomes 0, a share `neg_zero` of them -0.0 (0x8000)."""
+    rng = np.random.default_rng(seed)
+    bits = case.mask.buf
+    zero = np.where(rng.random(bits.shape) < neg_zero, np.uint16(0x8000), np.uint16(0))
+    bits[...] = np.where(bits == 0xFC00, np.uint16(0xFC00), zero)
+    return case
+
+
+@pytest.mark.parametrize("i,kw", list(enumerate([
+    dict(B=2, Sq=300, Nh=8, Nkv=2, Skv=517, p_masked=0.5),
+    dict(B=1, Sq=200, Nh=4, Nkv=4, Skv=450, mask_heads=4, p_masked=0.9, max_bias=8.0),
+    dict(B=1, Sq=256, Nh=8, Nkv=2, Skv=640, kv_type=30, p_masked=0.3),
+    dict(B=2, Sq=400, Nh=8, Nkv=4, Skv=250, p_masked=0.5),   # <= 4 key tiles: the 48-query kernel
+])))
+def test_binary_masks_against_mixed_tiles(mx, i, kw):
+    # Masks of 0 and -inf only, in random patterns (half the zeros -0.0).
+    # The classifier gives such (128-query x 64-key) tiles a 64-bit liveness
+    # word per row, and the 32-query prefill kernel then reads no mask
+    # element in them.  Checked at the parity bar against the oracle, and
+    # bit for bit against the same mask with one tiny non-zero value
+    # (0x0001, 2^-24) in every tile, which makes every tile mixed (mask read
+    # per element): equal on every row that value is not in.  Two variants
+    # put it in rows 128t and 128t + 1, so every row is compared once.
+    c = _binary_mask(_rand_case(900 + i, **kw), 950 + i)
+    got, _ = check(mx, c, f"binary mask {i}")
+    Skv, Sq, Hm, B = (int(x) for x in c.mask.ne)
+    n_kt = (Skv + 63) // 64
+    for c0 in (0, 1):
+        bits = c.mask.buf.reshape(B, Hm, Sq, Skv).copy()
+        rows = np.arange(c0, Sq, 128)
+        for t, r in enumerate(rows):
+            for u in range(n_kt):
+                bits[:, :, r, min(64 * u + (t + u) % 64, Skv - 1)] = 0x0001
+        mixed = replace(c, mask=replace(c.mask, buf=bits.reshape(-1)))
+        ref = run_gpu(mx, mixed)
+        keep = np.ones(Sq, dtype=bool)
+        keep[rows] = False
+        assert np.array_equal(got[:, keep].view(np.uint32), ref[:, keep].view(np.uint32)), \
+            (i, c0, float(np.abs(got[:, keep] - ref[:, keep]).max()))
 
 
 def test_workspace_grows_and_repeats(mx):
