@@ -450,36 +450,66 @@ def _binary_mask(case, seed, neg_zero=0.5):
 
 
 @pytest.mark.parametrize("i,kw", list(enumerate([
-    dict(B=2, Sq=300, Nh=8, Nkv=2, Skv=517, p_masked=0.5),
-    dict(B=1, Sq=200, Nh=4, Nkv=4, Skv=450, mask_heads=4, p_masked=0.9, max_bias=8.0),
+    dict(B=2, Sq=300, Nh=8, Nkv=2, Skv=516, p_masked=0.5),
+    dict(B=1, Sq=200, Nh=4, Nkv=4, Skv=452, mask_heads=4, p_masked=0.9, max_bias=8.0),
     dict(B=1, Sq=256, Nh=8, Nkv=2, Skv=640, kv_type=30, p_masked=0.3),
-    dict(B=2, Sq=400, Nh=8, Nkv=4, Skv=250, p_masked=0.5),   # <= 4 key tiles: the 48-query kernel
+    dict(B=2, Sq=400, Nh=8, Nkv=4, Skv=252, p_masked=0.5),   # <= 4 key tiles: the 48-query kernel
 ])))
 def test_binary_masks_against_mixed_tiles(mx, i, kw):
-    # Masks of 0 and -inf only, in random patterns (half the zeros -0.0).
-    # The classifier gives such (128-query x 64-key) tiles a 64-bit liveness
-    # word per row, and the 32-query prefill kernel then reads no mask
-    # element in them.  Checked at the parity bar against the oracle, and
-    # bit for bit against the same mask with one tiny non-zero value
-    # (0x0001, 2^-24) in every tile, which makes every tile mixed (mask read
-    # per element): equal on every row that value is not in.  Two variants
-    # put it in rows 128t and 128t + 1, so every row is compared once.
+    # Masks of 0 and -inf only, in random patterns (half the zeros -0.0),
+    # on the prefill kernels (rows of a multiple of 4 keys; the launch
+    # counter checks the route).  The classifier gives such (128-query x
+    # 64-key) tiles a 64-bit liveness word per row, and the 32-query kernel
+    # then reads no mask element in them.  Checked at the parity bar against
+    # the oracle, and bit for bit against the same mask with one live entry
+    # per tile set to 2^-24 (0x0001), which makes every tile mixed (mask read
+    # per element): equal on every row that value is not in.  The value goes
+    # into a live entry, so no row's live keys change; the second variant
+    # puts it only into rows the first left alone, so every row is compared.
+    import torch
+
     c = _binary_mask(_rand_case(900 + i, **kw), 950 + i)
-    got, _ = check(mx, c, f"binary mask {i}")
+    mx.timing_reset()
+    mx.timing_enable(True)
+    try:
+        got, _ = check(mx, c, f"binary mask {i}")
+        torch.cuda.synchronize()
+        assert mx.timing_read("fa_prefill")[1] == 1 and mx.timing_read("fa_decode")[1] == 0
+    finally:
+        mx.timing_enable(False)
+        mx.timing_reset()
     Skv, Sq, Hm, B = (int(x) for x in c.mask.ne)
-    n_kt = (Skv + 63) // 64
-    for c0 in (0, 1):
-        bits = c.mask.buf.reshape(B, Hm, Sq, Skv).copy()
-        rows = np.arange(c0, Sq, 128)
-        for t, r in enumerate(rows):
-            for u in range(n_kt):
-                bits[:, :, r, min(64 * u + (t + u) % 64, Skv - 1)] = 0x0001
+    Nh = int(c.q.ne[2])
+    planes = c.mask.buf.reshape(B, Hm, Sq, Skv)
+    compared = np.zeros((B, Sq, Nh), dtype=bool)
+    used = np.zeros((B, Hm, Sq), dtype=bool)   # mask rows the first variant perturbed
+    for var in (0, 1):
+        bits = planes.copy()
+        mine = np.zeros((B, Hm, Sq), dtype=bool)
+        for b in range(B):
+            for hm in range(Hm):
+                for q0 in range(0, Sq, 128):
+                    for k0 in range(0, Skv, 64):
+                        # the first row of the tile with a live key (second
+                        # variant: among the rows the first left alone)
+                        for r in range(q0, min(q0 + 128, Sq)):
+                            if var == 1 and used[b, hm, r]:
+                                continue
+                            live = np.flatnonzero(bits[b, hm, r, k0:k0 + 64] != 0xFC00)
+                            if live.size:
+                                bits[b, hm, r, k0 + live[0]] = 0x0001
+                                mine[b, hm, r] = True
+                                break
+        if var == 0:
+            used = mine
         mixed = replace(c, mask=replace(c.mask, buf=bits.reshape(-1)))
         ref = run_gpu(mx, mixed)
-        keep = np.ones(Sq, dtype=bool)
-        keep[rows] = False
-        assert np.array_equal(got[:, keep].view(np.uint32), ref[:, keep].view(np.uint32)), \
-            (i, c0, float(np.abs(got[:, keep] - ref[:, keep]).max()))
+        # output row (b, q, head) reads mask plane (b, head % Hm)
+        keep = ~mine[:, np.arange(Nh) % Hm, :].transpose(0, 2, 1)
+        assert np.array_equal(got[keep].view(np.uint32), ref[keep].view(np.uint32)), \
+            (i, var, float(np.abs(got[keep] - ref[keep]).max()))
+        compared |= keep
+    assert compared.all()
 
 
 def test_workspace_grows_and_repeats(mx):
