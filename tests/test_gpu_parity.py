@@ -290,6 +290,16 @@ def test_contiguous_q_and_no_mask(mx):
         check(mx, c, f"no mask contiguous q Sq={Sq}")
 
 
+@pytest.mark.parametrize("Skv", [1, 17, 64, 65, 130, 333, 1000])
+def test_short_decode_splits(mx, Skv):
+    # few streams over short windows: the LDS decode kernel (no mask) splits
+    # them into 64-key steps, the last split partial and its later waves
+    # idle; one and three query tokens, GQA 4:1
+    for Sq in (1, 3):
+        c = _rand_case(60 + Skv + Sq, B=2, Sq=Sq, Nh=8, Nkv=2, Skv=Skv, mask=None)
+        check(mx, c, f"short decode Skv={Skv} Sq={Sq}")
+
+
 @pytest.mark.parametrize("Sq,Skv,B,Bk,Nh,Nkv,mask,layout", [
     (64, 333, 1, 1, 4, 4, None, "perm"),        # one partial 192-query tile
     (193, 1000, 2, 1, 8, 2, None, "contig"),    # a 1-row second tile, KV batch broadcast, GQA 4:1
