@@ -67,7 +67,16 @@ __global__ void __launch_bounds__(256) mask_classify_kernel(const FaArgs a, uint
     // the live rows and keys, so no load needs a branch, and rows / keys
     // outside [0, Sq) x [0, Skv) are excluded afterwards by predicates.  The
     // loads go through a buffer resource over the mask plane.
-    const int kt = blockIdx.x, qt = blockIdx.y, plane = blockIdx.z;
+    // Tiles in (plane, query tile, key tile) order, key tile fastest; the
+    // 1D grid's workgroups go round-robin to the 8 XCDs, and XCD x takes the
+    // x-th contiguous eighth of the tiles: neighbouring key tiles of a row
+    // share the 128-byte lines their row pieces straddle (rows whose length
+    // is not a multiple of 128 bytes), and fetch them into one L2.
+    const uint32_t n_tiles = (uint32_t)a.n_kt * (uint32_t)a.n_qt * (uint32_t)(a.m_ne2 * a.m_ne3);
+    const uint32_t L = blockIdx.x, x = L % kXcds, per = n_tiles / kXcds, rem = n_tiles % kXcds;
+    const uint32_t T = x * per + min(x, rem) + L / kXcds;
+    const int kt = (int)(T % (uint32_t)a.n_kt), qt = (int)((T / (uint32_t)a.n_kt) % (uint32_t)a.n_qt);
+    const int plane = (int)(T / ((uint32_t)a.n_kt * (uint32_t)a.n_qt));
     const int m2i = plane % a.m_ne2, m3i = plane / a.m_ne2;
     // (the plane base is uniform; readfirstlane lets the compiler know, so
     // the buffer loads need no waterfall loop.  readfirstlane returns a
@@ -727,7 +736,9 @@ fa_prefill_q8q_kernel(const FaArgs a) {
 }
 
 hipError_t launch_mask_classify(const FaArgs &a, int n_planes, uint8_t *classes, hipStream_t stream) {
-    dim3 grid(a.n_kt, a.n_qt, n_planes);
+    // (1D over every tile of the n_planes = m_ne2 * m_ne3 mask planes)
+    if (n_planes != a.m_ne2 * a.m_ne3) return hipErrorInvalidValue;
+    dim3 grid((uint32_t)a.n_kt * (uint32_t)a.n_qt * (uint32_t)n_planes);
     hipLaunchKernelGGL(mask_classify_kernel, grid, dim3(256), 0, stream, a, classes);
     return hipGetLastError();
 }
