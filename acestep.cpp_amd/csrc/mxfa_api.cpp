@@ -91,7 +91,12 @@ constexpr bool kPfWide = MXFA_WIDE != 0;
 // follows the same rule as its dense form).
 constexpr int64_t kPfWideMaskedMaxKt = 4;
 // Workgroups the decode kernel aims for before it splits the KV range.
-constexpr int64_t kSplitTargetWgs = 512;
+// (build option for A/B runs; 512 = two workgroups per CU measured best:
+// 256, 384, 640, 768, 1024 and 2048 were slower on C3 / C5)
+#ifndef MXFA_SPLIT_TARGET
+#define MXFA_SPLIT_TARGET 512
+#endif
+constexpr int64_t kSplitTargetWgs = MXFA_SPLIT_TARGET;
 constexpr int kSplitKeyQuantum = 128;  // register kernel: 4 waves x 32 keys
 constexpr int kSplitKeyQuantumLds = 64;  // LDS kernel: 4 waves x 16 keys
 constexpr int64_t kMaxDecodeSplits = 64;   // merge capacity of the decode kernel
