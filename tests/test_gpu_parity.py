@@ -290,14 +290,15 @@ def test_contiguous_q_and_no_mask(mx):
         check(mx, c, f"no mask contiguous q Sq={Sq}")
 
 
-@pytest.mark.parametrize("Skv", [1, 17, 64, 65, 130, 333, 1000])
-def test_short_decode_splits(mx, Skv):
+@pytest.mark.parametrize("Skv,kv_type", [(1, 1), (17, 1), (64, 1), (65, 1), (130, 1), (333, 1), (1000, 1),
+                                         (65, 30), (333, 30)])
+def test_short_decode_splits(mx, Skv, kv_type):
     # few streams over short windows: the LDS decode kernel (no mask) splits
     # them into 64-key steps, the last split partial and its later waves
-    # idle; one and three query tokens, GQA 4:1
+    # idle; one and three query tokens, GQA 4:1, F16 and BF16
     for Sq in (1, 3):
-        c = _rand_case(60 + Skv + Sq, B=2, Sq=Sq, Nh=8, Nkv=2, Skv=Skv, mask=None)
-        check(mx, c, f"short decode Skv={Skv} Sq={Sq}")
+        c = _rand_case(60 + Skv + Sq, B=2, Sq=Sq, Nh=8, Nkv=2, Skv=Skv, kv_type=kv_type, mask=None)
+        check(mx, c, f"short decode Skv={Skv} Sq={Sq} type={kv_type}")
 
 
 @pytest.mark.parametrize("Sq,Skv,B,Bk,Nh,Nkv,mask,layout", [
