@@ -560,12 +560,14 @@ void make_plan(const mxfa_tensor *q, const mxfa_tensor *k, const mxfa_tensor *v,
     a.row_tiles = (a.M + 15) / 16;
     const int64_t base = (int64_t)a.B * a.Nkv * a.row_tiles;
     // Splits are whole steps of the kernel that runs them: 64 keys for the
-    // LDS kernel (F16/BF16 without a structured mask, no mask or one of
-    // 16-byte rows: 4 waves x 16 keys), 128 for the register kernel (4 x 32).
-    // Short windows then split finer: C1's 512 keys into 8 splits per KV head
-    // instead of 4, 9.67 -> 8.95 us per call, the 28-layer decode token
-    // 377.5 -> 355.3 us replayed (same box).
-    const bool lds_kernel = k->type != MXFA_TYPE_Q8_0 && !a.sm_flags && (!mask || a.mask_vec16);
+    // LDS kernel (F16/BF16 with no dense mask or one of 16-byte rows; a
+    // structured call has no dense mask: 4 waves x 16 keys), 128 for the
+    // register kernel (4 x 32).  Short windows then split finer: C1's 512
+    // keys into 8 splits per KV head instead of 4, 9.67 -> 8.95 us per call,
+    // the 28-layer decode token 377.5 -> 355.3 us replayed; structured
+    // splits of equal live work come closer to it: c3m 36.5-36.8 -> 35.9-36.0
+    // us (same box each).
+    const bool lds_kernel = k->type != MXFA_TYPE_Q8_0 && (!mask || a.mask_vec16);
     const int64_t quantum = lds_kernel ? kSplitKeyQuantumLds : kSplitKeyQuantum;
     const int64_t max_splits = (a.Skv + quantum - 1) / quantum;
     int64_t n_splits = 1, chunk = 0;
